@@ -1,0 +1,149 @@
+/*
+ * techjam_attn.h -- C ABI of the MI355X (gfx950) attention hot path.
+ *
+ * Plain pointers, sizes and a HIP stream; no framework types. Every tensor is
+ * described by a device pointer plus four element strides in the logical order
+ * [B, H, S, D]; the innermost (D) stride must be 1. Strided views -- for
+ * example the [B, S, H, D] and [B, S, 3, H, D] projection outputs seen as
+ * [B, H, S, D] -- are read in place, with no hidden copies.
+ *
+ * Conventions shared by all entry points:
+ *   - Work is enqueued on `stream`; no entry point synchronises the host.
+ *   - The caller owns and allocates every buffer (the library allocates no
+ *     device memory); kernels that need scratch space take a workspace.
+ *   - The return value is TJ_OK or one of the TJ_ERR_* codes below;
+ *     tj_error_string() names it. Argument checks happen before any launch.
+ *   - Calls are reentrant: the library keeps no mutable global state.
+ *
+ * The reference implements this path in Python on top of PyTorch SDPA and three
+ * Triton kernels; each declaration names the reference interface it replaces.
+ */
+#ifndef TECHJAM_ATTN_H
+#define TECHJAM_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Return codes. */
+#define TJ_OK 0
+#define TJ_ERR_SHAPE 1       /* inconsistent or non-positive sizes            */
+#define TJ_ERR_DTYPE 2       /* unsupported element type                      */
+#define TJ_ERR_ALIGN 3       /* pointer/stride not aligned for vector access  */
+#define TJ_ERR_UNSUPPORTED 4 /* valid request this build does not implement   */
+#define TJ_ERR_LAUNCH 5      /* the HIP runtime rejected a launch             */
+#define TJ_ERR_WORKSPACE 6   /* workspace missing or too small                */
+
+/* Element types of the tensor arguments. */
+#define TJ_F32 0
+#define TJ_F16 1
+
+/* ABI version, bumped on any signature or semantic change. */
+int tj_abi_version(void);
+
+/* Human-readable name of a return code. Never NULL. */
+const char* tj_error_string(int code);
+
+/*
+ * Exact scaled-dot-product attention, forward.
+ *
+ * Replaces torch.nn.functional.scaled_dot_product_attention as called by the
+ * reference at src/implementations/sdpa.py:65-73 and :157-165 (strided and
+ * packed-QKV views, is_causal, scale, key mask dropped under causal right
+ * padding), src/implementations/extreme.py:227-236 (forced-Flash fallback)
+ * and src/implementations/poly_reference.py:262-264 (exact prefix).
+ *
+ *   o[b,h,i,:] = sum_j softmax_j(scale * q[b,h,i,:].k[b,h,j,:]) v[b,h,j,:]
+ *
+ * over keys j < valid_len[b] (all keys when valid_len is NULL) and, when
+ * `causal`, j <= i. Rows i >= valid_len[b] are written as zeros: those are
+ * the padded query rows the model zeroes after its output projection
+ * (torch_transformer_benchmark.py:120-121). When row_limit is non-NULL, only
+ * rows i < row_limit[b*H + h] are computed and written; the other rows of o
+ * are left untouched (the polynomial path fills them).
+ *
+ * Arithmetic: q, k, v are rounded to fp16 (q after multiplying by
+ * scale*log2(e)); QK^T and PV run on fp16 MFMA with fp32 accumulation; the
+ * online softmax runs in fp32 on base-2 exponentials; o is written in the
+ * input type. head_dim D must be 32, 64 or 128.
+ *
+ * dtype: TJ_F32 or TJ_F16 (q, k, v and o share it).
+ * valid_len: device int32[B] or NULL. row_limit: device int32[B*H] or NULL.
+ */
+int tj_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype,
+                int64_t B, int64_t H, int64_t S, int64_t D,
+                const int64_t q_strides[4], const int64_t k_strides[4],
+                const int64_t v_strides[4], const int64_t o_strides[4],
+                float scale, int causal, const int32_t* valid_len,
+                const int32_t* row_limit, hipStream_t stream);
+
+/*
+ * Device-side score guard of the polynomial route.
+ *
+ * Replaces estimate_sigma / poly_is_safe / hermite_coefficients
+ * (src/implementations/poly_guard.py:68-102,
+ * src/implementations/poly_reference.py:35-58) and the module-level sigma cache
+ * of src/implementations/extreme.py:299-305, without the host synchronisation:
+ * for every (b,h) it takes the n_samples rows listed in sample_idx (device
+ * int32), forms all n_samples^2 scaled scores q_s.k_s * scale and writes
+ *   sigma_out[bh]  : their Bessel-corrected standard deviation,
+ *   smax_out[bh]   : their largest magnitude,
+ *   flags_out[bh]  : 1 when 0 < sigma <= ceiling and finite (polynomial route),
+ *                    0 otherwise (exact fallback),
+ *   coeffs_out[3*bh..]: (c0, c1, c2) of the Hermite fit at that sigma,
+ *   row_limit_out[bh]: min(exact_prefix, S) for flagged heads, S otherwise --
+ *                    the rows tj_attn_fwd must compute for that head.
+ * Any output pointer except flags_out may be NULL.
+ */
+int tj_score_guard(const void* q, const void* k, int dtype,
+                   int64_t B, int64_t H, int64_t S, int64_t D,
+                   const int64_t q_strides[4], const int64_t k_strides[4],
+                   float scale, const int32_t* sample_idx, int64_t n_samples,
+                   float ceiling, int64_t exact_prefix,
+                   float* sigma_out, float* smax_out, int32_t* flags_out,
+                   float* coeffs_out, int32_t* row_limit_out, hipStream_t stream);
+
+/*
+ * Workspace needed by tj_poly_attn_fwd, in bytes.
+ */
+size_t tj_poly_workspace_bytes(int64_t B, int64_t H, int64_t S, int64_t D, int64_t chunk);
+
+/*
+ * Causal degree-2 polynomial linear attention, rows >= exact_prefix.
+ *
+ * Replaces poly_attention_forward -> poly_linear_attention
+ * (src/implementations/poly_attention.py:21-83,
+ * src/implementations/poly_reference.py:61-265) together with the three Triton
+ * kernels quad_apply / quad_update / causal_diag
+ * (src/kernels/poly_attention_triton.py:420-591). With a = q*sqrt(scale) and
+ * b = k*sqrt(scale), every chunk of `chunk` tokens that ends past
+ * exact_prefix gets
+ *   o = (c0*S_const + c1*a.S_lin + c2*phi2(a).S_quad + diag_num)
+ *     / (c0*t0     + c1*a.z_lin + c2*a^T G a        + diag_den)
+ * with the diagonal block exp(a_i.b_j), j <= i inside the chunk, evaluated
+ * exactly (no max subtraction), and the fp32 states folded forward chunk by
+ * chunk. Operands are fp16, accumulation and states fp32.
+ *
+ * coeffs: device float[B*H*3] (c0, c1, c2 per head). flags: device int32[B*H]
+ * or NULL; heads with flags[bh] == 0 are skipped entirely. Rows < exact_prefix
+ * are not written: compute them with tj_attn_fwd (row_limit from the guard).
+ * Only D == 64 and chunk == 512 are implemented.
+ */
+int tj_poly_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype,
+                     int64_t B, int64_t H, int64_t S, int64_t D,
+                     const int64_t q_strides[4], const int64_t k_strides[4],
+                     const int64_t v_strides[4], const int64_t o_strides[4],
+                     float scale, int64_t chunk, int64_t exact_prefix,
+                     const float* coeffs, const int32_t* flags,
+                     void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TECHJAM_ATTN_H */

@@ -1,0 +1,22 @@
+"""CPU restatement of the reference's attention hot path -- TEST INFRASTRUCTURE.
+
+This package is the checker, never the product. Only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import it. The ``techjam_amd`` package must not import anything from here; its
+attention always runs the HIP kernels and fails loudly when they are missing.
+
+Modules and the reference code each one restates:
+
+* ``model``     -- dense pre-norm Transformer, seeded inputs and the OR-rule
+                   checker (``torch_transformer_benchmark.py:29-356``).
+* ``attention`` -- exact attention: fp64 brute force, and the blockwise
+                   online-softmax "linear-memory FP32 oracle"
+                   (``src/implementations/fp32_reference.py:70-204``).
+* ``poly``      -- degree-2 polynomial linear attention, Hermite coefficients
+                   and the sigma guard (``src/implementations/poly_reference.py:30-265``,
+                   ``src/implementations/poly_guard.py:65-102``).
+
+Every function is pinned by a test in ``tests/test_oracle_*.py`` against a
+closed form, an invariant, a brute-force computation or a known answer taken
+from the reference's own tests. Nothing here is "parity unpinned".
+"""

@@ -1,0 +1,352 @@
+// Exact causal / right-padded scaled-dot-product attention for gfx950.
+//
+// Forward pass of softmax(q k^T * scale) v with FP32 (or FP16) tensors in HBM,
+// fp16 MFMA operands and fp32 accumulation; replaces the SDPA calls of the
+// reference (src/implementations/sdpa.py:65-73, :157-165,
+// src/implementations/extreme.py:227-236, poly_reference.py:262-264).
+//
+// Work decomposition
+//   * One workgroup = 4 waves = a tile of 128 query rows of one (b, h); each
+//     wave owns 32 consecutive rows for the whole key loop.
+//   * Keys stream through LDS in tiles of 64 (double buffered): K row-major,
+//     V transposed, both converted to fp16 while being stored.
+//   * Scores are computed transposed, S^T = K Q^T (keys x queries), so a lane
+//     holds 32 keys of ONE query: the row max/sum is lane-local plus one swap
+//     with lane ^ 32, the rescale factor is a per-lane scalar, and the fp32
+//     accumulator converts in place into the B operand of O^T = V^T P^T -- P
+//     never leaves registers.
+//   * Q is pre-multiplied by scale*log2(e) before rounding, so the softmax runs
+//     on exp2 with no per-score multiply.
+//   * Causal tiles above the diagonal are never loaded; a wave skips the
+//     compute of tiles that start after its last row. Under causal attention
+//     the right-padding key mask is redundant (every valid row i only sees
+//     keys j <= i < L) and is not applied; padded rows i >= L are written as 0.
+//   * Grid: tile ids are remapped so that all query tiles of one (b, h) land on
+//     one XCD (K/V stay in that XCD's L2), heaviest (last) query tile first.
+#include "tj_common.h"
+
+namespace tj {
+namespace {
+
+constexpr int BM = 128;    // query rows per workgroup
+constexpr int BN = 64;     // keys per tile
+constexpr int NT = 256;    // threads per workgroup
+constexpr int PAD = 8;     // fp16 padding per LDS row (16 bytes)
+
+struct AttnArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  View4 vq, vk, vv, vo;
+  int B, H, S;
+  float qscale;  // scale * log2(e)
+  int causal;
+  const int32_t* valid_len;
+  const int32_t* row_limit;
+  int n_mtiles;
+  int total_tiles;
+  int per_xcd;
+};
+
+template <typename T, int HD>
+struct Tile {
+  static constexpr int VEC = Vec16<T>::N;      // elements per 16-byte load
+  static constexpr int NC = HD / VEC;          // 16-byte vectors per row
+  static constexpr int UNITS = 16 * NC;        // (4-key group, vector) units
+  static constexpr int UPT = (UNITS + NT - 1) / NT;
+  static constexpr int KS = HD / 16;           // MFMA k-steps over head_dim
+  static constexpr int DB = HD / 32;           // 32-wide output blocks
+  static_assert(NC % 4 == 0, "head_dim too small for the load mapping");
+};
+
+template <typename T, int HD>
+struct Smem {
+  half_t k[2][BN][HD + PAD];   // K tile, row-major
+  half_t vt[2][HD][BN + PAD];  // V tile, transposed, columns in key_slot order
+};
+
+// Global -> register staging of one key tile. Unit u covers keys 4g .. 4g+3 of
+// the tile and one 16-byte column vector c; lanes 4n .. 4n+3 share g so a
+// 16-lane LDS store phase touches 4 rows x 4 columns.
+template <typename T, int HD>
+struct KVStage {
+  using TL = Tile<T, HD>;
+  Vec16<T> kx[TL::UPT][4];
+  Vec16<T> vx[TL::UPT][4];
+
+  __device__ __forceinline__ static void unit_coords(int u, int& g, int& c) {
+    g = (u >> 2) & 15;
+    c = (u & 3) | ((u >> 6) << 2);
+  }
+
+  __device__ __forceinline__ void load(const AttnArgs& a, int b, int h, int kv0, int tid) {
+    const T* kp = reinterpret_cast<const T*>(a.k);
+    const T* vp = reinterpret_cast<const T*>(a.v);
+#pragma unroll
+    for (int p = 0; p < TL::UPT; ++p) {
+      const int u = tid + p * NT;
+      if (u < TL::UNITS) {
+        int g, c;
+        unit_coords(u, g, c);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = kv0 + 4 * g + r;
+          if (key < a.S) {
+            kx[p][r].load(kp + a.vk.row(b, h, key) + c * TL::VEC);
+            vx[p][r].load(vp + a.vv.row(b, h, key) + c * TL::VEC);
+          } else {
+            kx[p][r].zero();
+            vx[p][r].zero();
+          }
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(Smem<T, HD>& sm, int buf, int tid) const {
+#pragma unroll
+    for (int p = 0; p < TL::UPT; ++p) {
+      const int u = tid + p * NT;
+      if (u < TL::UNITS) {
+        int g, c;
+        unit_coords(u, g, c);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+#pragma unroll
+          for (int e = 0; e < TL::VEC; e += 4) {
+            half4_t hk = {(half_t)kx[p][r].get(e), (half_t)kx[p][r].get(e + 1),
+                          (half_t)kx[p][r].get(e + 2), (half_t)kx[p][r].get(e + 3)};
+            *reinterpret_cast<half4_t*>(&sm.k[buf][4 * g + r][c * TL::VEC + e]) = hk;
+          }
+        }
+        const int slot = key_slot(4 * g);
+#pragma unroll
+        for (int e = 0; e < TL::VEC; ++e) {
+          half4_t hv = {(half_t)vx[p][0].get(e), (half_t)vx[p][1].get(e),
+                        (half_t)vx[p][2].get(e), (half_t)vx[p][3].get(e)};
+          *reinterpret_cast<half4_t*>(&sm.vt[buf][c * TL::VEC + e][slot]) = hv;
+        }
+      }
+    }
+  }
+};
+
+template <typename T, int HD>
+__global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnArgs a) {
+  using TL = Tile<T, HD>;
+  __shared__ Smem<T, HD> sm;
+
+  // XCD-aware tile order: ids x, x+8, x+16, ... run on XCD x and take
+  // consecutive logical tiles, i.e. all query tiles of a few (b, h).
+  const int id = blockIdx.x;
+  const int logical = (id % kNumXcd) * a.per_xcd + id / kNumXcd;
+  if (logical >= a.total_tiles) return;
+  const int bh = logical / a.n_mtiles;
+  const int mt = a.n_mtiles - 1 - logical % a.n_mtiles;
+  const int b = bh / a.H;
+  const int h = bh % a.H;
+  const int q0 = mt * BM;
+  int row_cap = a.S;
+  if (a.row_limit != nullptr) row_cap = min(row_cap, max(0, a.row_limit[bh]));
+  if (q0 >= row_cap) return;
+  int L = a.S;
+  if (a.valid_len != nullptr) L = min(a.S, max(0, a.valid_len[b]));
+
+  const int tid = threadIdx.x;
+  const int w = tid / kWave;
+  const int lane = tid % kWave;
+  const int hl = lane / 32;
+  const int ln = lane % 32;
+  const int qw0 = q0 + 32 * w;
+  const int qi = qw0 + ln;
+
+  const int kv_end = a.causal ? min(q0 + BM, L) : L;
+  const int n_kv = kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
+  // Last key this wave needs (inclusive); waves whose rows are all padding
+  // (or beyond row_cap) compute nothing.
+  int wave_last_key = a.causal ? min(qw0 + 31, kv_end - 1) : kv_end - 1;
+  if (qw0 >= L || qw0 >= row_cap) wave_last_key = -1;
+
+  // Q^T as the B operand: lane holds query qi, dims 16*ks + 8*hl .. +7.
+  half8_t qf[TL::KS];
+  {
+    const T* qp = reinterpret_cast<const T*>(a.q);
+    const bool in = qi < a.S;
+    const int64_t base = a.vq.row(b, h, in ? qi : 0);
+#pragma unroll
+    for (int ks = 0; ks < TL::KS; ++ks) {
+      const int d0 = 16 * ks + 8 * hl;
+#pragma unroll
+      for (int e = 0; e < 8; e += Vec16<T>::N) {
+        Vec16<T> x;
+        if (in) x.load(qp + base + d0 + e); else x.zero();
+#pragma unroll
+        for (int j = 0; j < Vec16<T>::N; ++j) qf[ks][e + j] = (half_t)(x.get(j) * a.qscale);
+      }
+    }
+  }
+
+  float16_t oacc[TL::DB];
+#pragma unroll
+  for (int db = 0; db < TL::DB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[db][r] = 0.f;
+  float m_run = -__builtin_inff();
+  float l_run = 0.f;
+
+  KVStage<T, HD> stage;
+  if (n_kv > 0) {
+    stage.load(a, b, h, 0, tid);
+    stage.store(sm, 0, tid);
+  }
+  __syncthreads();
+
+  for (int kt = 0; kt < n_kv; ++kt) {
+    const int cur = kt & 1;
+    const int kv0 = kt * BN;
+    if (kt + 1 < n_kv) stage.load(a, b, h, kv0 + BN, tid);
+
+    if (kv0 <= wave_last_key) {
+      float16_t sacc[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < TL::KS; ++ks) {
+          const half8_t kf = *reinterpret_cast<const half8_t*>(&sm.k[cur][kb * 32 + ln][16 * ks + 8 * hl]);
+          sacc[kb] = mfma32(kf, qf[ks], sacc[kb]);
+        }
+      }
+      // Mask keys past the diagonal (causal) or past the valid length.
+      const bool need_mask = a.causal ? (kv0 + BN - 1 > qw0) : (kv0 + BN > L);
+      if (need_mask) {
+        const int lim = a.causal ? qi : L - 1;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = kv0 + kb * 32 + 8 * (r / 4) + 4 * hl + (r % 4);
+            if (key > lim) sacc[kb][r] = -__builtin_inff();
+          }
+      }
+      float mt_loc = sacc[0][0];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mt_loc = fmaxf(mt_loc, sacc[kb][r]);
+      mt_loc = fmaxf(mt_loc, xor32(mt_loc));
+      const float m_new = fmaxf(m_run, mt_loc);
+      const float alpha = fast_exp2(m_run - m_new);
+      m_run = m_new;
+      float psum = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p = fast_exp2(sacc[kb][r] - m_new);
+          sacc[kb][r] = p;
+          psum += p;
+        }
+      l_run = l_run * alpha + psum;
+#pragma unroll
+      for (int db = 0; db < TL::DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+      // O^T += V^T P^T over four 16-key steps.
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int kb = s / 2;
+        const int r0 = 8 * (s % 2);
+        half8_t pf;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pf[j] = (half_t)sacc[kb][r0 + j];
+#pragma unroll
+        for (int db = 0; db < TL::DB; ++db) {
+          const half8_t vf = *reinterpret_cast<const half8_t*>(&sm.vt[cur][db * 32 + ln][16 * s + 8 * hl]);
+          oacc[db] = mfma32(vf, pf, oacc[db]);
+        }
+      }
+    }
+
+    if (kt + 1 < n_kv) stage.store(sm, cur ^ 1, tid);
+    __syncthreads();
+  }
+
+  // Epilogue: combine the two half-row sums, normalise, store.
+  const float l_tot = l_run + xor32(l_run);
+  if (qi < row_cap) {
+    const float inv = (qi < L && l_tot > 0.f) ? 1.f / l_tot : 0.f;
+    T* op = reinterpret_cast<T*>(a.o) + a.vo.row(b, h, qi);
+#pragma unroll
+    for (int db = 0; db < TL::DB; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = db * 32 + 8 * g + 4 * hl;
+        if constexpr (sizeof(T) == 4) {
+          float4_t v4 = {oacc[db][4 * g] * inv, oacc[db][4 * g + 1] * inv, oacc[db][4 * g + 2] * inv,
+                         oacc[db][4 * g + 3] * inv};
+          *reinterpret_cast<float4_t*>(op + d0) = v4;
+        } else {
+          half4_t v4 = {(half_t)(oacc[db][4 * g] * inv), (half_t)(oacc[db][4 * g + 1] * inv),
+                        (half_t)(oacc[db][4 * g + 2] * inv), (half_t)(oacc[db][4 * g + 3] * inv)};
+          *reinterpret_cast<half4_t*>(op + d0) = v4;
+        }
+      }
+  }
+}
+
+template <typename T, int HD>
+int launch(const AttnArgs& a, hipStream_t stream) {
+  const int grid = a.per_xcd * kNumXcd;
+  hipLaunchKernelGGL((attn_fwd_kernel<T, HD>), dim3(grid), dim3(NT), 0, stream, a);
+  return tjh::launch_status();
+}
+
+template <typename T>
+int dispatch_hd(const AttnArgs& a, int64_t D, hipStream_t stream) {
+  switch (D) {
+    case 32: return launch<T, 32>(a, stream);
+    case 64: return launch<T, 64>(a, stream);
+    case 128: return launch<T, 128>(a, stream);
+    default: return TJ_ERR_UNSUPPORTED;
+  }
+}
+
+}  // namespace
+}  // namespace tj
+
+extern "C" int tj_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype,
+                           int64_t B, int64_t H, int64_t S, int64_t D,
+                           const int64_t q_strides[4], const int64_t k_strides[4],
+                           const int64_t v_strides[4], const int64_t o_strides[4],
+                           float scale, int causal, const int32_t* valid_len,
+                           const int32_t* row_limit, hipStream_t stream) {
+  if (dtype != TJ_F32 && dtype != TJ_F16) return TJ_ERR_DTYPE;
+  if (B < 0 || H <= 0 || S < 0 || D <= 0) return TJ_ERR_SHAPE;
+  if (B * H * ((S + 127) / 128) >= (int64_t(1) << 31)) return TJ_ERR_SHAPE;
+  if (D != 32 && D != 64 && D != 128) return TJ_ERR_UNSUPPORTED;
+  if (B == 0 || S == 0) return TJ_OK;
+  if (!q || !k || !v || !o) return TJ_ERR_SHAPE;
+  if (!tjh::view_ok(q, q_strides, dtype) || !tjh::view_ok(k, k_strides, dtype) ||
+      !tjh::view_ok(v, v_strides, dtype) || !tjh::view_ok(o, o_strides, dtype))
+    return TJ_ERR_ALIGN;
+
+  tj::AttnArgs a;
+  a.q = q; a.k = k; a.v = v; a.o = o;
+  a.vq = {q_strides[0], q_strides[1], q_strides[2]};
+  a.vk = {k_strides[0], k_strides[1], k_strides[2]};
+  a.vv = {v_strides[0], v_strides[1], v_strides[2]};
+  a.vo = {o_strides[0], o_strides[1], o_strides[2]};
+  a.B = (int)B; a.H = (int)H; a.S = (int)S;
+  a.qscale = scale * 1.4426950408889634f;
+  a.causal = causal ? 1 : 0;
+  a.valid_len = valid_len;
+  a.row_limit = row_limit;
+  a.n_mtiles = (int)((S + tj::BM - 1) / tj::BM);
+  a.total_tiles = (int)(B * H) * a.n_mtiles;
+  a.per_xcd = (a.total_tiles + tj::kNumXcd - 1) / tj::kNumXcd;
+  if (dtype == TJ_F32) return tj::dispatch_hd<float>(a, D, stream);
+  return tj::dispatch_hd<half_t>(a, D, stream);
+}

@@ -1,0 +1,99 @@
+// Shared types and helpers of the gfx950 attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "techjam_attn.h"
+
+typedef _Float16 half_t;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float8_t __attribute__((ext_vector_type(8)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+namespace tj {
+
+constexpr int kWave = 64;
+constexpr int kNumXcd = 8;  // MI355X: 8 XCDs, workgroups dispatched round-robin
+
+// 32x32x16 fp16 MFMA (gfx950): D = A * B + C.
+//   A: lane l holds row (l % 32), k-slots 8*(l/32) .. +7
+//   B: lane l holds column (l % 32), k-slots 8*(l/32) .. +7
+//   C/D: lane l, register r holds row 8*(r/4) + 4*(l/32) + (r%4), column (l % 32)
+// The contraction is a sum over k, so any slot -> k assignment works as long
+// as A and B use the same one; the kernels rely on that to feed accumulators
+// back as operands without a shuffle.
+__device__ __forceinline__ float16_t mfma32(half8_t a, half8_t b, float16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32, kWave); }
+
+// 16-byte vector of input elements: 4 floats or 8 halves, widened to fp32.
+template <typename T>
+struct Vec16;
+
+template <>
+struct Vec16<float> {
+  static constexpr int N = 4;
+  float4_t v;
+  __device__ __forceinline__ void load(const float* p) { v = *reinterpret_cast<const float4_t*>(p); }
+  __device__ __forceinline__ void zero() { v = float4_t{0.f, 0.f, 0.f, 0.f}; }
+  __device__ __forceinline__ float get(int i) const { return v[i]; }
+};
+
+template <>
+struct Vec16<half_t> {
+  static constexpr int N = 8;
+  half8_t v;
+  __device__ __forceinline__ void load(const half_t* p) { v = *reinterpret_cast<const half8_t*>(p); }
+  __device__ __forceinline__ void zero() { v = half8_t{0, 0, 0, 0, 0, 0, 0, 0}; }
+  __device__ __forceinline__ float get(int i) const { return (float)v[i]; }
+};
+
+// Strided [B, H, S, D] view with unit D stride.
+struct View4 {
+  int64_t sb, sh, ss;
+  __device__ __forceinline__ int64_t row(int b, int h, int s) const {
+    return (int64_t)b * sb + (int64_t)h * sh + (int64_t)s * ss;
+  }
+};
+
+// Swap bits 2 and 3 of a key index inside each 16-key group. The exact
+// kernel stores V^T columns in this order so that the eight keys one lane
+// contributes to a PV k-step sit in one 16-byte LDS word (see attn_exact.hip).
+__device__ __forceinline__ int key_slot(int key) {
+  return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
+}
+
+}  // namespace tj
+
+// Host-side argument checks shared by the entry points.
+namespace tjh {
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline int elem_size(int dtype) { return dtype == TJ_F32 ? 4 : (dtype == TJ_F16 ? 2 : 0); }
+
+// Row starts of a strided view are 16-byte aligned when the base is and every
+// outer stride is a multiple of 16 bytes.
+inline bool view_ok(const void* p, const int64_t st[4], int dtype) {
+  const int64_t vec = 16 / elem_size(dtype);
+  if (st == nullptr || st[3] != 1) return false;
+  if (!aligned16(p)) return false;
+  for (int i = 0; i < 3; ++i)
+    if (st[i] % vec != 0) return false;
+  return true;
+}
+
+inline int launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? TJ_OK : TJ_ERR_LAUNCH;
+}
+
+}  // namespace tjh

@@ -1,0 +1,121 @@
+"""The C-ABI library builds, loads without a GPU and exports what the header declares.
+
+No kernel is launched here: only entry points that reject their arguments
+before touching the HIP runtime are called.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "techjam_attn.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tj_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_path_entry_points():
+    names = declared_functions()
+    for required in ("tj_attn_fwd", "tj_score_guard", "tj_poly_attn_fwd",
+                     "tj_poly_workspace_bytes", "tj_error_string", "tj_abi_version"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    from techjam_amd.kernels import _lib
+
+    handle = _lib.lib()
+    for name in declared_functions():
+        assert hasattr(handle, name), name
+    # and the binding describes each one
+    assert set(declared_functions()) == set(_lib.SIGNATURES)
+
+
+def test_error_strings_are_distinct_and_never_null():
+    from techjam_amd.kernels import _lib
+
+    texts = {_lib.error_text(c) for c in range(0, 7)}
+    assert len(texts) == 7
+    assert _lib.error_text(12345) == "unknown error"
+
+
+def test_abi_version():
+    from techjam_amd.kernels import _lib
+
+    assert _lib.lib().tj_abi_version() == 1
+
+
+def _strides(*s):
+    return (ctypes.c_int64 * 4)(*s)
+
+
+def test_attn_rejects_bad_arguments_before_launching():
+    from techjam_amd.kernels import _lib
+
+    L = _lib.lib()
+    st = _strides(64 * 128 * 4, 64, 64 * 4, 1)
+    args = [16, 16, 16, 16]  # fake aligned pointers: never dereferenced on these paths
+    # unsupported dtype
+    assert L.tj_attn_fwd(*args, 7, 1, 4, 128, 64, st, st, st, st, 0.125, 1, None, None, None) == _lib.TJ_ERR_DTYPE
+    # unsupported head dim
+    assert L.tj_attn_fwd(*args, _lib.TJ_F32, 1, 4, 128, 48, st, st, st, st, 0.125, 1, None, None, None) == _lib.TJ_ERR_UNSUPPORTED
+    # negative sizes
+    assert L.tj_attn_fwd(*args, _lib.TJ_F32, -1, 4, 128, 64, st, st, st, st, 0.125, 1, None, None, None) == _lib.TJ_ERR_SHAPE
+    # innermost stride != 1
+    bad = _strides(64 * 128 * 4, 64, 64 * 4, 2)
+    assert L.tj_attn_fwd(*args, _lib.TJ_F32, 1, 4, 128, 64, bad, st, st, st, 0.125, 1, None, None, None) == _lib.TJ_ERR_ALIGN
+    # misaligned base pointer
+    assert L.tj_attn_fwd(4, 16, 16, 16, _lib.TJ_F32, 1, 4, 128, 64, st, st, st, st, 0.125, 1, None, None, None) == _lib.TJ_ERR_ALIGN
+    # row stride not a multiple of 16 bytes
+    odd = _strides(64 * 128 * 4, 64, 66, 1)
+    assert L.tj_attn_fwd(*args, _lib.TJ_F32, 1, 4, 128, 64, st, odd, st, st, 0.125, 1, None, None, None) == _lib.TJ_ERR_ALIGN
+    # empty problems are a successful no-op
+    assert L.tj_attn_fwd(*args, _lib.TJ_F32, 0, 4, 128, 64, st, st, st, st, 0.125, 1, None, None, None) == _lib.TJ_OK
+
+
+def test_guard_rejects_bad_arguments_before_launching():
+    from techjam_amd.kernels import _lib
+
+    L = _lib.lib()
+    st = _strides(64 * 128 * 4, 64, 64 * 4, 1)
+    # more samples than rows
+    assert L.tj_score_guard(16, 16, _lib.TJ_F32, 1, 4, 128, 64, st, st, 0.125, 16, 256, 0.4, 64,
+                            None, None, 16, None, None, None) == _lib.TJ_ERR_SHAPE
+    # missing flags output
+    assert L.tj_score_guard(16, 16, _lib.TJ_F32, 1, 4, 128, 64, st, st, 0.125, 16, 64, 0.4, 64,
+                            None, None, None, None, None, None) == _lib.TJ_ERR_SHAPE
+    assert L.tj_score_guard(16, 16, _lib.TJ_F32, 1, 4, 128, 256, st, st, 0.125, 16, 64, 0.4, 64,
+                            None, None, 16, None, None, None) == _lib.TJ_ERR_UNSUPPORTED
+
+
+def test_check_maps_codes_to_reference_exceptions():
+    from techjam_amd.errors import UnsupportedCaseError
+    from techjam_amd.kernels import _lib
+
+    _lib.check(_lib.TJ_OK, "x")
+    for code in (_lib.TJ_ERR_SHAPE, _lib.TJ_ERR_DTYPE, _lib.TJ_ERR_ALIGN, _lib.TJ_ERR_WORKSPACE):
+        with pytest.raises(ValueError):
+            _lib.check(code, "x")
+    with pytest.raises(UnsupportedCaseError):
+        _lib.check(_lib.TJ_ERR_UNSUPPORTED, "x")
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.TJ_ERR_LAUNCH, "x")
+
+
+def test_cpu_tensors_are_refused_not_computed():
+    import torch
+
+    from techjam_amd.errors import UnsupportedCaseError
+    from techjam_amd.kernels import scaled_dot_product_attention
+
+    q = torch.randn(1, 2, 16, 64)
+    with pytest.raises(UnsupportedCaseError):
+        scaled_dot_product_attention(q, q, q, is_causal=True)

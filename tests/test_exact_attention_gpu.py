@@ -1,0 +1,167 @@
+"""Parity of the HIP exact-attention kernel with the oracle (GPU).
+
+The oracle is ``oracle.attention``: float64 brute force for small shapes and
+the blockwise online softmax in float64 on the CPU for larger ones. Inputs are
+drawn on the CPU from seeded generators and copied to the GPU. The bar is the
+benchmark's per-element rule ``|d| <= 2e-3 OR |d| <= 0.02*|ref|`` with zero
+failures (``torch_transformer_benchmark.py:309-319``); fp16 operands with fp32
+accumulation sit far inside it, so the tests also bound the max abs error.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.attention import blockwise_attention, brute_force_attention
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-3, 0.02
+
+
+def _draw(shape, seed, scale=1.0, dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g, dtype=torch.float64) * scale).to(dtype)
+
+
+def _assert_close(got: torch.Tensor, ref, max_abs=None, what=""):
+    got = got.detach().double().cpu().numpy()
+    ref = np.asarray(ref, dtype=np.float64)
+    err = np.abs(got - ref)
+    ok = np.isfinite(got) & ((err <= ATOL) | (err <= RTOL * np.abs(ref)))
+    n_bad = int((~ok).sum())
+    assert n_bad == 0, f"{what}: {n_bad} failing elements, max abs err {err.max():.3e}"
+    if max_abs is not None:
+        assert err.max() <= max_abs, f"{what}: max abs err {err.max():.3e} > {max_abs}"
+
+
+def _run(q, k, v, dev, **kw):
+    from techjam_amd.kernels import scaled_dot_product_attention
+
+    out = scaled_dot_product_attention(q.to(dev), k.to(dev), v.to(dev), **kw)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("s", [1, 7, 64, 100, 129, 300])
+def test_matches_brute_force(cuda, s, causal, d):
+    b, h = 2, 3
+    q, k, v = (_draw((b, h, s, d), seed) for seed in (1, 2, 3))
+    ref = brute_force_attention(q, k, v, d ** -0.5, causal)
+    got = _run(q, k, v, cuda, is_causal=causal)
+    _assert_close(got, ref, max_abs=4e-3, what=f"s={s} d={d} causal={causal}")
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_right_padding_valid_lengths(cuda, causal):
+    b, h, s, d = 4, 2, 200, 64
+    q, k, v = (_draw((b, h, s, d), seed) for seed in (4, 5, 6))
+    lengths = [200, 77, 1, 0]
+    ref = brute_force_attention(q, k, v, d ** -0.5, causal, valid_len=lengths)
+    vl = torch.tensor(lengths, dtype=torch.int32, device=cuda)
+    got = _run(q, k, v, cuda, is_causal=causal, valid_len=vl)
+    _assert_close(got, ref, max_abs=4e-3, what=f"valid_len causal={causal}")
+    # padded rows are exact zeros
+    for bi, n in enumerate(lengths):
+        assert torch.count_nonzero(got[bi, :, n:]).item() == 0
+
+
+def test_row_limit_leaves_other_rows_untouched(cuda):
+    from techjam_amd.kernels import scaled_dot_product_attention
+
+    b, h, s, d = 2, 3, 300, 64
+    q, k, v = (_draw((b, h, s, d), seed) for seed in (7, 8, 9))
+    limits = torch.tensor([0, 1, 128, 129, 300, 1000], dtype=torch.int32)
+    out = torch.full((b, h, s, d), 12345.0, device=cuda)
+    scaled_dot_product_attention(q.to(cuda), k.to(cuda), v.to(cuda), is_causal=True,
+                                 row_limit=limits.to(cuda), out=out)
+    torch.cuda.synchronize()
+    ref = brute_force_attention(q, k, v, d ** -0.5, True)
+    got = out.cpu()
+    for bh in range(b * h):
+        bi, hi = divmod(bh, h)
+        n = min(int(limits[bh]), s)
+        _assert_close(got[bi, hi, :n], ref[bi, hi, :n], what=f"head {bh}")
+        assert bool((got[bi, hi, n:] == 12345.0).all()), f"head {bh} rows >= {n} were written"
+
+
+def test_packed_qkv_strided_views(cuda):
+    """q, k, v as views of one [B, S, 3, H, D] projection; output into [B, S, H, D]."""
+    b, s, h, d = 2, 333, 4, 64
+    packed = _draw((b, s, 3, h, d), 10)
+    q, k, v = (packed[:, :, i].transpose(1, 2) for i in range(3))
+    ref = brute_force_attention(q, k, v, d ** -0.5, True)
+    from techjam_amd.kernels import scaled_dot_product_attention
+
+    pk = packed.to(cuda)
+    qg, kg, vg = (pk[:, :, i].transpose(1, 2) for i in range(3))
+    assert qg.stride() == (s * 3 * h * d, d, 3 * h * d, 1)
+    got = scaled_dot_product_attention(qg, kg, vg, is_causal=True)
+    torch.cuda.synchronize()
+    assert got.transpose(1, 2).is_contiguous()  # [B, S, H, D] storage, free reshape
+    _assert_close(got, ref, max_abs=4e-3, what="packed views")
+
+
+def test_float16_inputs(cuda):
+    b, h, s, d = 2, 2, 257, 64
+    q, k, v = (_draw((b, h, s, d), seed).half() for seed in (11, 12, 13))
+    ref = brute_force_attention(q.double(), k.double(), v.double(), d ** -0.5, True)
+    got = _run(q, k, v, cuda, is_causal=True)
+    assert got.dtype == torch.float16
+    _assert_close(got.float(), ref, max_abs=4e-3, what="fp16")
+
+
+@pytest.mark.parametrize("scale_in", [0.1, 2.0, 6.0])
+def test_large_and_small_score_ranges(cuda, scale_in):
+    """Peaked softmax (max subtraction matters) and nearly flat softmax."""
+    b, h, s, d = 1, 2, 256, 64
+    q, k = (_draw((b, h, s, d), seed, scale_in) for seed in (14, 15))
+    v = _draw((b, h, s, d), 16)
+    ref = brute_force_attention(q, k, v, d ** -0.5, True)
+    got = _run(q, k, v, cuda, is_causal=True)
+    _assert_close(got, ref, what=f"input scale {scale_in}")
+
+
+def test_long_sequence_against_blockwise_oracle(cuda):
+    b, h, s, d = 1, 2, 4096, 64
+    q, k, v = (_draw((b, h, s, d), seed) for seed in (17, 18, 19))
+    ref = blockwise_attention(q.double(), k.double(), v.double(), d ** -0.5, True, acc_dtype=torch.float64)
+    got = _run(q, k, v, cuda, is_causal=True)
+    _assert_close(got, ref.numpy(), max_abs=4e-3, what="S=4096")
+
+
+def test_deterministic_and_strictly_causal(cuda):
+    from techjam_amd.kernels import scaled_dot_product_attention
+
+    b, h, s, d = 1, 2, 512, 64
+    q, k, v = (_draw((b, h, s, d), seed).to(cuda) for seed in (20, 21, 22))
+    a1 = scaled_dot_product_attention(q, k, v, is_causal=True)
+    a2 = scaled_dot_product_attention(q, k, v, is_causal=True)
+    k2, v2 = k.clone(), v.clone()
+    k2[:, :, 300:] *= 7.0
+    v2[:, :, 300:] *= 7.0
+    a3 = scaled_dot_product_attention(q, k2, v2, is_causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(a1, a2)
+    assert torch.equal(a1[:, :, :300], a3[:, :, :300])
+    assert not torch.equal(a1[:, :, 300:], a3[:, :, 300:])
+
+
+def test_full_benchmark_shape_sampled_heads(cuda):
+    """B=64, S=4096, H=16, D=64 causal (the attention-core workload); a few heads checked."""
+    from techjam_amd.kernels import scaled_dot_product_attention
+
+    b, s, h, d = 64, 4096, 16, 64
+    g = torch.Generator(device=cuda).manual_seed(101234)
+    q, k, v = (torch.randn(b, s, h, d, generator=g, device=cuda).transpose(1, 2) for _ in range(3))
+    out = scaled_dot_product_attention(q, k, v, is_causal=True)
+    torch.cuda.synchronize()
+    for bi, hi in ((0, 0), (63, 15), (17, 9)):
+        ref = blockwise_attention(q[bi:bi + 1, hi:hi + 1].double().cpu(), k[bi:bi + 1, hi:hi + 1].double().cpu(),
+                                  v[bi:bi + 1, hi:hi + 1].double().cpu(), d ** -0.5, True,
+                                  block_q=2048, block_k=2048, acc_dtype=torch.float64)
+        _assert_close(out[bi:bi + 1, hi:hi + 1], ref.numpy(), max_abs=4e-3, what=f"head ({bi},{hi})")
