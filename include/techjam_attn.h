@@ -70,17 +70,22 @@ const char* tj_error_string(int code);
  * Arithmetic: q, k, v are rounded to fp16 (q after multiplying by
  * scale*log2(e)); QK^T and PV run on fp16 MFMA with fp32 accumulation; the
  * online softmax runs in fp32 on base-2 exponentials; o is written in the
- * input type. head_dim D must be 32, 64 or 128.
+ * input type. Heads with qk_split[b*H + h] != 0 form QK^T from a two-term
+ * fp16 expansion of q and k (three MFMAs), which keeps fp32-level score
+ * accuracy for wide score ranges (sigma of the scaled scores >~ 2).
+ * head_dim D must be 32, 64 or 128.
  *
  * dtype: TJ_F32 or TJ_F16 (q, k, v and o share it).
- * valid_len: device int32[B] or NULL. row_limit: device int32[B*H] or NULL.
+ * valid_len: device int32[B] or NULL. row_limit, qk_split: device
+ * int32[B*H] or NULL.
  */
 int tj_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype,
                 int64_t B, int64_t H, int64_t S, int64_t D,
                 const int64_t q_strides[4], const int64_t k_strides[4],
                 const int64_t v_strides[4], const int64_t o_strides[4],
                 float scale, int causal, const int32_t* valid_len,
-                const int32_t* row_limit, hipStream_t stream);
+                const int32_t* row_limit, const int32_t* qk_split,
+                hipStream_t stream);
 
 /*
  * Device-side score guard of the polynomial route.
@@ -97,7 +102,9 @@ int tj_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype,
  *                    0 otherwise (exact fallback),
  *   coeffs_out[3*bh..]: (c0, c1, c2) of the Hermite fit at that sigma,
  *   row_limit_out[bh]: min(exact_prefix, S) for flagged heads, S otherwise --
- *                    the rows tj_attn_fwd must compute for that head.
+ *                    the rows tj_attn_fwd must compute for that head,
+ *   split_out[bh]  : 1 for heads routed to the exact fallback (their score
+ *                    range is wide), 0 otherwise -- tj_attn_fwd's qk_split.
  * Any output pointer except flags_out may be NULL.
  */
 int tj_score_guard(const void* q, const void* k, int dtype,
@@ -106,7 +113,8 @@ int tj_score_guard(const void* q, const void* k, int dtype,
                    float scale, const int32_t* sample_idx, int64_t n_samples,
                    float ceiling, int64_t exact_prefix,
                    float* sigma_out, float* smax_out, int32_t* flags_out,
-                   float* coeffs_out, int32_t* row_limit_out, hipStream_t stream);
+                   float* coeffs_out, int32_t* row_limit_out, int32_t* split_out,
+                   hipStream_t stream);
 
 /*
  * Workspace needed by tj_poly_attn_fwd, in bytes.

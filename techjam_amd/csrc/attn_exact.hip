@@ -23,6 +23,10 @@
 //     keys j <= i < L) and is not applied; padded rows i >= L are written as 0.
 //   * Grid: tile ids are remapped so that all query tiles of one (b, h) land on
 //     one XCD (K/V stay in that XCD's L2), heaviest (last) query tile first.
+//   * Heads flagged in qk_split compute QK^T from a two-term fp16 expansion of
+//     q and k (x = hi + lo, both fp16) with three MFMAs -- hi.hi + hi.lo +
+//     lo.hi -- which restores fp32-level score accuracy where the score range
+//     is wide enough for fp16 rounding of q and k to show in the softmax.
 #include "tj_common.h"
 
 namespace tj {
@@ -44,6 +48,7 @@ struct AttnArgs {
   int causal;
   const int32_t* valid_len;
   const int32_t* row_limit;
+  const int32_t* qk_split;
   int n_mtiles;
   int total_tiles;
   int per_xcd;
@@ -60,10 +65,19 @@ struct Tile {
   static_assert(NC % 4 == 0, "head_dim too small for the load mapping");
 };
 
-template <typename T, int HD>
-struct Smem {
-  half_t k[2][BN][HD + PAD];   // K tile, row-major
+template <int HD>
+struct SmemBase {
+  half_t k[2][BN][HD + PAD];   // K tile (high part), row-major
   half_t vt[2][HD][BN + PAD];  // V tile, transposed, columns in key_slot order
+};
+
+// Kernels that may meet split heads also carry the low part of K.
+template <int HD, bool SPLIT_OK>
+struct Smem : SmemBase<HD> {};
+
+template <int HD>
+struct Smem<HD, true> : SmemBase<HD> {
+  half_t klo[2][BN][HD + PAD];
 };
 
 // Global -> register staging of one key tile. Unit u covers keys 4g .. 4g+3 of
@@ -104,7 +118,8 @@ struct KVStage {
     }
   }
 
-  __device__ __forceinline__ void store(Smem<T, HD>& sm, int buf, int tid) const {
+  template <bool SPLIT, typename SM>
+  __device__ __forceinline__ void store(SM& sm, int buf, int tid) const {
 #pragma unroll
     for (int p = 0; p < TL::UPT; ++p) {
       const int u = tid + p * NT;
@@ -115,9 +130,15 @@ struct KVStage {
         for (int r = 0; r < 4; ++r) {
 #pragma unroll
           for (int e = 0; e < TL::VEC; e += 4) {
-            half4_t hk = {(half_t)kx[p][r].get(e), (half_t)kx[p][r].get(e + 1),
-                          (half_t)kx[p][r].get(e + 2), (half_t)kx[p][r].get(e + 3)};
+            half4_t hk, lk;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const float x = kx[p][r].get(e + j);
+              hk[j] = (half_t)x;
+              lk[j] = (half_t)(x - (float)hk[j]);
+            }
             *reinterpret_cast<half4_t*>(&sm.k[buf][4 * g + r][c * TL::VEC + e]) = hk;
+            if constexpr (SPLIT) *reinterpret_cast<half4_t*>(&sm.klo[buf][4 * g + r][c * TL::VEC + e]) = lk;
           }
         }
         const int slot = key_slot(4 * g);
@@ -132,27 +153,11 @@ struct KVStage {
   }
 };
 
-template <typename T, int HD>
-__global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnArgs a) {
+// One query tile of one (b, h). SPLIT selects the three-MFMA score path.
+template <typename T, int HD, bool SPLIT, typename SM>
+__device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int h, int q0, int row_cap,
+                                          int L) {
   using TL = Tile<T, HD>;
-  __shared__ Smem<T, HD> sm;
-
-  // XCD-aware tile order: ids x, x+8, x+16, ... run on XCD x and take
-  // consecutive logical tiles, i.e. all query tiles of a few (b, h).
-  const int id = blockIdx.x;
-  const int logical = (id % kNumXcd) * a.per_xcd + id / kNumXcd;
-  if (logical >= a.total_tiles) return;
-  const int bh = logical / a.n_mtiles;
-  const int mt = a.n_mtiles - 1 - logical % a.n_mtiles;
-  const int b = bh / a.H;
-  const int h = bh % a.H;
-  const int q0 = mt * BM;
-  int row_cap = a.S;
-  if (a.row_limit != nullptr) row_cap = min(row_cap, max(0, a.row_limit[bh]));
-  if (q0 >= row_cap) return;
-  int L = a.S;
-  if (a.valid_len != nullptr) L = min(a.S, max(0, a.valid_len[b]));
-
   const int tid = threadIdx.x;
   const int w = tid / kWave;
   const int lane = tid % kWave;
@@ -170,6 +175,7 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnArgs a) {
 
   // Q^T as the B operand: lane holds query qi, dims 16*ks + 8*hl .. +7.
   half8_t qf[TL::KS];
+  half8_t qlo[SPLIT ? TL::KS : 1];
   {
     const T* qp = reinterpret_cast<const T*>(a.q);
     const bool in = qi < a.S;
@@ -182,7 +188,12 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnArgs a) {
         Vec16<T> x;
         if (in) x.load(qp + base + d0 + e); else x.zero();
 #pragma unroll
-        for (int j = 0; j < Vec16<T>::N; ++j) qf[ks][e + j] = (half_t)(x.get(j) * a.qscale);
+        for (int j = 0; j < Vec16<T>::N; ++j) {
+          const float y = x.get(j) * a.qscale;
+          const half_t hi = (half_t)y;
+          qf[ks][e + j] = hi;
+          if constexpr (SPLIT) qlo[ks][e + j] = (half_t)(y - (float)hi);
+        }
       }
     }
   }
@@ -198,7 +209,7 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnArgs a) {
   KVStage<T, HD> stage;
   if (n_kv > 0) {
     stage.load(a, b, h, 0, tid);
-    stage.store(sm, 0, tid);
+    stage.template store<SPLIT>(sm, 0, tid);
   }
   __syncthreads();
 
@@ -216,6 +227,11 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
         for (int ks = 0; ks < TL::KS; ++ks) {
           const half8_t kf = *reinterpret_cast<const half8_t*>(&sm.k[cur][kb * 32 + ln][16 * ks + 8 * hl]);
+          if constexpr (SPLIT) {
+            const half8_t kl = *reinterpret_cast<const half8_t*>(&sm.klo[cur][kb * 32 + ln][16 * ks + 8 * hl]);
+            sacc[kb] = mfma32(kl, qf[ks], sacc[kb]);
+            sacc[kb] = mfma32(kf, qlo[ks], sacc[kb]);
+          }
           sacc[kb] = mfma32(kf, qf[ks], sacc[kb]);
         }
       }
@@ -270,7 +286,7 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnArgs a) {
       }
     }
 
-    if (kt + 1 < n_kv) stage.store(sm, cur ^ 1, tid);
+    if (kt + 1 < n_kv) stage.template store<SPLIT>(sm, cur ^ 1, tid);
     __syncthreads();
   }
 
@@ -297,10 +313,42 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnArgs a) {
   }
 }
 
+template <typename T, int HD, bool SPLIT_OK>
+__global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnArgs a) {
+  __shared__ Smem<HD, SPLIT_OK> sm;
+
+  // XCD-aware tile order: ids x, x+8, x+16, ... run on XCD x and take
+  // consecutive logical tiles, i.e. all query tiles of a few (b, h).
+  const int id = blockIdx.x;
+  const int logical = (id % kNumXcd) * a.per_xcd + id / kNumXcd;
+  if (logical >= a.total_tiles) return;
+  const int bh = logical / a.n_mtiles;
+  const int mt = a.n_mtiles - 1 - logical % a.n_mtiles;
+  const int b = bh / a.H;
+  const int h = bh % a.H;
+  const int q0 = mt * BM;
+  int row_cap = a.S;
+  if (a.row_limit != nullptr) row_cap = min(row_cap, max(0, a.row_limit[bh]));
+  if (q0 >= row_cap) return;
+  int L = a.S;
+  if (a.valid_len != nullptr) L = min(a.S, max(0, a.valid_len[b]));
+
+  if constexpr (SPLIT_OK) {
+    if (a.qk_split[bh] != 0) {
+      attn_tile<T, HD, true>(a, sm, b, h, q0, row_cap, L);
+      return;
+    }
+  }
+  attn_tile<T, HD, false>(a, sm, b, h, q0, row_cap, L);
+}
+
 template <typename T, int HD>
 int launch(const AttnArgs& a, hipStream_t stream) {
   const int grid = a.per_xcd * kNumXcd;
-  hipLaunchKernelGGL((attn_fwd_kernel<T, HD>), dim3(grid), dim3(NT), 0, stream, a);
+  if (a.qk_split != nullptr)
+    hipLaunchKernelGGL((attn_fwd_kernel<T, HD, true>), dim3(grid), dim3(NT), 0, stream, a);
+  else
+    hipLaunchKernelGGL((attn_fwd_kernel<T, HD, false>), dim3(grid), dim3(NT), 0, stream, a);
   return tjh::launch_status();
 }
 
@@ -322,7 +370,7 @@ extern "C" int tj_attn_fwd(const void* q, const void* k, const void* v, void* o,
                            const int64_t q_strides[4], const int64_t k_strides[4],
                            const int64_t v_strides[4], const int64_t o_strides[4],
                            float scale, int causal, const int32_t* valid_len,
-                           const int32_t* row_limit, hipStream_t stream) {
+                           const int32_t* row_limit, const int32_t* qk_split, hipStream_t stream) {
   if (dtype != TJ_F32 && dtype != TJ_F16) return TJ_ERR_DTYPE;
   if (B < 0 || H <= 0 || S < 0 || D <= 0) return TJ_ERR_SHAPE;
   if (B * H * ((S + 127) / 128) >= (int64_t(1) << 31)) return TJ_ERR_SHAPE;
@@ -344,6 +392,7 @@ extern "C" int tj_attn_fwd(const void* q, const void* k, const void* v, void* o,
   a.causal = causal ? 1 : 0;
   a.valid_len = valid_len;
   a.row_limit = row_limit;
+  a.qk_split = qk_split;
   a.n_mtiles = (int)((S + tj::BM - 1) / tj::BM);
   a.total_tiles = (int)(B * H) * a.n_mtiles;
   a.per_xcd = (a.total_tiles + tj::kNumXcd - 1) / tj::kNumXcd;

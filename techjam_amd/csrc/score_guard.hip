@@ -36,6 +36,7 @@ struct GuardArgs {
   int32_t* flags;
   float* coeffs;
   int32_t* row_limit;
+  int32_t* split;
 };
 
 // Stage up to GB sampled rows, transposed: dst[d][r] = src[idx[r0 + r], d] * mul.
@@ -147,6 +148,7 @@ __global__ __launch_bounds__(GT) void score_guard_kernel(GuardArgs a) {
       a.coeffs[3 * bh + 2] = (float)(0.5 * g);
     }
     if (a.row_limit) a.row_limit[bh] = safe ? min(a.exact_prefix, a.S) : a.S;
+    if (a.split) a.split[bh] = safe ? 0 : 1;
   }
 }
 
@@ -159,7 +161,8 @@ extern "C" int tj_score_guard(const void* q, const void* k, int dtype,
                               float scale, const int32_t* sample_idx, int64_t n_samples,
                               float ceiling, int64_t exact_prefix,
                               float* sigma_out, float* smax_out, int32_t* flags_out,
-                              float* coeffs_out, int32_t* row_limit_out, hipStream_t stream) {
+                              float* coeffs_out, int32_t* row_limit_out, int32_t* split_out,
+                              hipStream_t stream) {
   if (dtype != TJ_F32 && dtype != TJ_F16) return TJ_ERR_DTYPE;
   if (B <= 0 || H <= 0 || S <= 0 || D <= 0 || n_samples <= 0 || n_samples > S) return TJ_ERR_SHAPE;
   if (D > tj::GMAXD) return TJ_ERR_UNSUPPORTED;
@@ -176,6 +179,7 @@ extern "C" int tj_score_guard(const void* q, const void* k, int dtype,
   a.idx = sample_idx;
   a.sigma = sigma_out; a.smax = smax_out; a.flags = flags_out; a.coeffs = coeffs_out;
   a.row_limit = row_limit_out;
+  a.split = split_out;
   const dim3 grid((unsigned)(B * H));
   if (dtype == TJ_F32)
     hipLaunchKernelGGL(tj::score_guard_kernel<float>, grid, dim3(tj::GT), 0, stream, a);

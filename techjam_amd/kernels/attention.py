@@ -13,7 +13,7 @@ from __future__ import annotations
 
 import ctypes
 from dataclasses import dataclass
-from typing import Optional
+from typing import Optional, Union
 
 import torch
 
@@ -93,6 +93,7 @@ def scaled_dot_product_attention(
     scale: Optional[float] = None,
     valid_len: Optional[torch.Tensor] = None,
     row_limit: Optional[torch.Tensor] = None,
+    qk_split: Union[bool, torch.Tensor, None] = None,
     out: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Exact attention on the HIP kernel; ``[B, H, S, D]`` views in, ``[B, H, S, D]`` out.
@@ -101,7 +102,9 @@ def scaled_dot_product_attention(
     and zeroes rows ``i >= valid_len[b]``: the right-padding contract of the
     model, where those rows are zeroed after the output projection anyway.
     ``row_limit`` (int32 ``[B*H]``) restricts the rows computed per head; the
-    other rows of ``out`` are left untouched.
+    other rows of ``out`` are left untouched. ``qk_split`` (``True`` for all
+    heads, or an int32 ``[B*H]`` device flag tensor) selects the three-MFMA
+    score path that keeps fp32-level score accuracy for wide score ranges.
     """
     _check_qkv(q, k, v)
     dev = _require_device(q, k, v)
@@ -113,7 +116,12 @@ def scaled_dot_product_attention(
         out = empty_like_heads(q)
     elif out.shape != q.shape or out.dtype != q.dtype or out.device != dev:
         raise ValueError("out must match q in shape, dtype and device")
-    for name, t, n in (("valid_len", valid_len, b), ("row_limit", row_limit, b * h)):
+    if qk_split is True:
+        qk_split = _all_heads(b * h, dev)
+    elif qk_split is False:
+        qk_split = None
+    for name, t, n in (("valid_len", valid_len, b), ("row_limit", row_limit, b * h),
+                       ("qk_split", qk_split, b * h)):
         if t is not None and (t.dtype != torch.int32 or t.device != dev or t.numel() != n
                               or not t.is_contiguous()):
             raise ValueError(f"{name} must be a contiguous int32 tensor of {n} elements on {dev}")
@@ -121,10 +129,23 @@ def scaled_dot_product_attention(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), _DTYPES[q.dtype],
         b, h, s, d,
         _lib.strides4(q), _lib.strides4(k), _lib.strides4(v), _lib.strides4(out),
-        float(scale), int(bool(is_causal)), _ptr(valid_len), _ptr(row_limit), _stream_ptr(dev),
+        float(scale), int(bool(is_causal)), _ptr(valid_len), _ptr(row_limit), _ptr(qk_split),
+        _stream_ptr(dev),
     )
     _lib.check(code, "tj_attn_fwd")
     return out
+
+
+_ONES: dict = {}
+
+
+def _all_heads(n: int, dev: torch.device) -> torch.Tensor:
+    key = (n, str(dev))
+    t = _ONES.get(key)
+    if t is None:
+        t = torch.ones(n, dtype=torch.int32, device=dev)
+        _ONES[key] = t
+    return t
 
 
 @dataclass
@@ -136,6 +157,7 @@ class GuardResult:
     flags: torch.Tensor       # int32   [B*H], 1 = polynomial route
     coeffs: torch.Tensor      # float32 [B*H, 3]
     row_limit: torch.Tensor   # int32   [B*H], rows the exact kernel computes
+    split: torch.Tensor       # int32   [B*H], 1 = exact fallback with split scores
 
 
 _SAMPLE_CACHE: dict = {}
@@ -185,13 +207,14 @@ def score_guard(
         flags=torch.empty(m, dtype=torch.int32, device=dev),
         coeffs=torch.empty(m, 3, dtype=torch.float32, device=dev),
         row_limit=torch.empty(m, dtype=torch.int32, device=dev),
+        split=torch.empty(m, dtype=torch.int32, device=dev),
     )
     code = _lib.lib().tj_score_guard(
         q.data_ptr(), k.data_ptr(), _DTYPES[q.dtype], b, h, s, d,
         _lib.strides4(q), _lib.strides4(k), float(scale), idx.data_ptr(), idx.numel(),
         float(ceiling), int(exact_prefix),
         res.sigma.data_ptr(), res.smax.data_ptr(), res.flags.data_ptr(),
-        res.coeffs.data_ptr(), res.row_limit.data_ptr(), _stream_ptr(dev),
+        res.coeffs.data_ptr(), res.row_limit.data_ptr(), res.split.data_ptr(), _stream_ptr(dev),
     )
     _lib.check(code, "tj_score_guard")
     return res

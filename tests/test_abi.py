@@ -64,21 +64,21 @@ def test_attn_rejects_bad_arguments_before_launching():
     st = _strides(64 * 128 * 4, 64, 64 * 4, 1)
     args = [16, 16, 16, 16]  # fake aligned pointers: never dereferenced on these paths
     # unsupported dtype
-    assert L.tj_attn_fwd(*args, 7, 1, 4, 128, 64, st, st, st, st, 0.125, 1, None, None, None) == _lib.TJ_ERR_DTYPE
+    assert L.tj_attn_fwd(*args, 7, 1, 4, 128, 64, st, st, st, st, 0.125, 1, None, None, None, None) == _lib.TJ_ERR_DTYPE
     # unsupported head dim
-    assert L.tj_attn_fwd(*args, _lib.TJ_F32, 1, 4, 128, 48, st, st, st, st, 0.125, 1, None, None, None) == _lib.TJ_ERR_UNSUPPORTED
+    assert L.tj_attn_fwd(*args, _lib.TJ_F32, 1, 4, 128, 48, st, st, st, st, 0.125, 1, None, None, None, None) == _lib.TJ_ERR_UNSUPPORTED
     # negative sizes
-    assert L.tj_attn_fwd(*args, _lib.TJ_F32, -1, 4, 128, 64, st, st, st, st, 0.125, 1, None, None, None) == _lib.TJ_ERR_SHAPE
+    assert L.tj_attn_fwd(*args, _lib.TJ_F32, -1, 4, 128, 64, st, st, st, st, 0.125, 1, None, None, None, None) == _lib.TJ_ERR_SHAPE
     # innermost stride != 1
     bad = _strides(64 * 128 * 4, 64, 64 * 4, 2)
-    assert L.tj_attn_fwd(*args, _lib.TJ_F32, 1, 4, 128, 64, bad, st, st, st, 0.125, 1, None, None, None) == _lib.TJ_ERR_ALIGN
+    assert L.tj_attn_fwd(*args, _lib.TJ_F32, 1, 4, 128, 64, bad, st, st, st, 0.125, 1, None, None, None, None) == _lib.TJ_ERR_ALIGN
     # misaligned base pointer
-    assert L.tj_attn_fwd(4, 16, 16, 16, _lib.TJ_F32, 1, 4, 128, 64, st, st, st, st, 0.125, 1, None, None, None) == _lib.TJ_ERR_ALIGN
+    assert L.tj_attn_fwd(4, 16, 16, 16, _lib.TJ_F32, 1, 4, 128, 64, st, st, st, st, 0.125, 1, None, None, None, None) == _lib.TJ_ERR_ALIGN
     # row stride not a multiple of 16 bytes
     odd = _strides(64 * 128 * 4, 64, 66, 1)
-    assert L.tj_attn_fwd(*args, _lib.TJ_F32, 1, 4, 128, 64, st, odd, st, st, 0.125, 1, None, None, None) == _lib.TJ_ERR_ALIGN
+    assert L.tj_attn_fwd(*args, _lib.TJ_F32, 1, 4, 128, 64, st, odd, st, st, 0.125, 1, None, None, None, None) == _lib.TJ_ERR_ALIGN
     # empty problems are a successful no-op
-    assert L.tj_attn_fwd(*args, _lib.TJ_F32, 0, 4, 128, 64, st, st, st, st, 0.125, 1, None, None, None) == _lib.TJ_OK
+    assert L.tj_attn_fwd(*args, _lib.TJ_F32, 0, 4, 128, 64, st, st, st, st, 0.125, 1, None, None, None, None) == _lib.TJ_OK
 
 
 def test_guard_rejects_bad_arguments_before_launching():
@@ -88,12 +88,12 @@ def test_guard_rejects_bad_arguments_before_launching():
     st = _strides(64 * 128 * 4, 64, 64 * 4, 1)
     # more samples than rows
     assert L.tj_score_guard(16, 16, _lib.TJ_F32, 1, 4, 128, 64, st, st, 0.125, 16, 256, 0.4, 64,
-                            None, None, 16, None, None, None) == _lib.TJ_ERR_SHAPE
+                            None, None, 16, None, None, None, None) == _lib.TJ_ERR_SHAPE
     # missing flags output
     assert L.tj_score_guard(16, 16, _lib.TJ_F32, 1, 4, 128, 64, st, st, 0.125, 16, 64, 0.4, 64,
-                            None, None, None, None, None, None) == _lib.TJ_ERR_SHAPE
+                            None, None, None, None, None, None, None) == _lib.TJ_ERR_SHAPE
     assert L.tj_score_guard(16, 16, _lib.TJ_F32, 1, 4, 128, 256, st, st, 0.125, 16, 64, 0.4, 64,
-                            None, None, 16, None, None, None) == _lib.TJ_ERR_UNSUPPORTED
+                            None, None, 16, None, None, None, None) == _lib.TJ_ERR_UNSUPPORTED
 
 
 def test_check_maps_codes_to_reference_exceptions():
