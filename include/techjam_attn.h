@@ -97,6 +97,7 @@ int tj_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype,
  * for every (b,h) it takes the n_samples rows listed in sample_idx (device
  * int32), forms all n_samples^2 scaled scores q_s.k_s * scale and writes
  *   sigma_out[bh]  : their Bessel-corrected standard deviation,
+ *   mean_out[bh]   : their mean (with sigma, the moments pooled estimates need),
  *   smax_out[bh]   : their largest magnitude,
  *   flags_out[bh]  : 1 when 0 < sigma <= ceiling and finite (polynomial route),
  *                    0 otherwise (exact fallback),
@@ -112,7 +113,7 @@ int tj_score_guard(const void* q, const void* k, int dtype,
                    const int64_t q_strides[4], const int64_t k_strides[4],
                    float scale, const int32_t* sample_idx, int64_t n_samples,
                    float ceiling, int64_t exact_prefix,
-                   float* sigma_out, float* smax_out, int32_t* flags_out,
+                   float* sigma_out, float* mean_out, float* smax_out, int32_t* flags_out,
                    float* coeffs_out, int32_t* row_limit_out, int32_t* split_out,
                    hipStream_t stream);
 

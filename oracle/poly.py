@@ -133,10 +133,14 @@ def poly_linear_attention(
                 den = c0 * float(t0) + c1 * (a @ z_lin.to(cdt)).to(sdt)
                 den = den + c2 * ((a @ gram.to(cdt)) * a).sum(-1, keepdim=True).to(sdt)
             if diag_hook is None:
+                # exp and the row sum run in at least fp32 (in fp64 for an fp64 scan); the
+                # weights are rounded to the compute dtype before the PV product, and the
+                # denominator sums the same rounded weights.
+                wide = torch.promote_types(cdt, torch.float32)
                 upper = torch.ones(c, c, dtype=torch.bool, device=dev).triu(1)
-                w = torch.exp((a @ b.transpose(-2, -1)).float()).masked_fill(upper, 0.0).to(cdt)
+                w = torch.exp((a @ b.transpose(-2, -1)).to(wide)).masked_fill(upper, 0.0).to(cdt)
                 d_num = w @ vc
-                d_den = w.float().sum(-1, keepdim=True)
+                d_den = w.to(wide).sum(-1, keepdim=True)
             else:
                 d_num, d_den = diag_hook(a, b, vc)
             num = num + d_num.to(sdt)

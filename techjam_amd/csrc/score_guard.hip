@@ -32,6 +32,7 @@ struct GuardArgs {
   int exact_prefix;
   const int32_t* idx;
   float* sigma;
+  float* mean;
   float* smax;
   int32_t* flags;
   float* coeffs;
@@ -138,6 +139,7 @@ __global__ __launch_bounds__(GT) void score_guard_kernel(GuardArgs a) {
     const double sigma = sqrt(var);
     const bool safe = isfinite(sigma) && sigma > 0.0 && sigma <= (double)a.ceiling;
     if (a.sigma) a.sigma[bh] = (float)sigma;
+    if (a.mean) a.mean[bh] = (float)(cnt > 0.0 ? s1 / cnt : 0.0);
     if (a.smax) a.smax[bh] = m;
     a.flags[bh] = safe ? 1 : 0;
     if (a.coeffs) {
@@ -160,7 +162,7 @@ extern "C" int tj_score_guard(const void* q, const void* k, int dtype,
                               const int64_t q_strides[4], const int64_t k_strides[4],
                               float scale, const int32_t* sample_idx, int64_t n_samples,
                               float ceiling, int64_t exact_prefix,
-                              float* sigma_out, float* smax_out, int32_t* flags_out,
+                              float* sigma_out, float* mean_out, float* smax_out, int32_t* flags_out,
                               float* coeffs_out, int32_t* row_limit_out, int32_t* split_out,
                               hipStream_t stream) {
   if (dtype != TJ_F32 && dtype != TJ_F16) return TJ_ERR_DTYPE;
@@ -177,7 +179,7 @@ extern "C" int tj_score_guard(const void* q, const void* k, int dtype,
   a.scale = scale; a.ceiling = ceiling;
   a.exact_prefix = (int)(exact_prefix < 0 ? 0 : (exact_prefix > S ? S : exact_prefix));
   a.idx = sample_idx;
-  a.sigma = sigma_out; a.smax = smax_out; a.flags = flags_out; a.coeffs = coeffs_out;
+  a.sigma = sigma_out; a.mean = mean_out; a.smax = smax_out; a.flags = flags_out; a.coeffs = coeffs_out;
   a.row_limit = row_limit_out;
   a.split = split_out;
   const dim3 grid((unsigned)(B * H));

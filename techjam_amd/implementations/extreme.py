@@ -1,0 +1,190 @@
+"""Memory-bounded execution for extreme shapes and the guarded polynomial module.
+
+Mirrors ``src/implementations/extreme.py:18-319``:
+
+* ``choose_batch_chunk_size`` / ``estimate_batch_chunk_size`` (``:40-117``):
+  largest power-of-two batch chunk whose working set fits a fraction of HBM.
+  The HIP kernels never materialise scores, so the dispatcher calls them with
+  ``score_copies=0``; the parameter stays for the reference's callers.
+* ``right_padded_lengths`` (``:120-133``), ``forward_batch_chunks`` with OOM
+  halving (``:136-164``) and ``forward_prefix_chunks`` with trimmed equal-length
+  groups (``:167-204``).
+* ``ExactOnlySelfAttention`` -- the forced exact fallback (the reference's
+  ``FlashOnlySDPASelfAttention``, ``:207-238``): mask-free, padding trimmed by
+  the caller, FP32 or FP16 interface.
+* ``PolyOrExactSelfAttention`` -- the guarded route (``PolyOrFlashSelfAttention``,
+  ``:249-319``) with the guard evaluated per head on the device instead of one
+  cached host-side sigma.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Callable
+from typing import Optional
+
+import torch
+
+from ..kernels.attention import scaled_dot_product_attention
+from .poly_attention import guarded_attention
+from .poly_guard import poly_is_safe
+from .sdpa import StridedSDPASelfAttention
+
+CASE_6_CONFIG = (10000, 128, 128, 4, 128, True, 4)
+CASE_14_CONFIG = (32, 100000, 1024, 16, 1024, True, 2)
+DEFAULT_MEMORY_FRACTION = 0.85
+
+ChunkForward = Callable[[torch.Tensor, Optional[torch.Tensor]], torch.Tensor]
+
+# One switch returns the guarded modules to exact attention on every head.
+POLY_ATTENTION_ENABLED = True
+
+
+def choose_batch_chunk_size(x: torch.Tensor, num_heads: int, *, score_copies: int, activation_copies: int,
+                            memory_fraction: float = DEFAULT_MEMORY_FRACTION) -> int:
+    """Largest power-of-two batch chunk inside a conservative device-memory budget."""
+    if not 0.0 < memory_fraction <= 1.0:
+        raise ValueError("memory_fraction must be in (0, 1]")
+    if num_heads <= 0:
+        raise ValueError("num_heads must be positive")
+    if score_copies < 0 or activation_copies <= 0:
+        raise ValueError("memory-copy estimates must be non-negative")
+    if x.shape[0] <= 1 or x.device.type != "cuda":
+        return 1
+    free_bytes, total_bytes = torch.cuda.mem_get_info(x.device)
+    allocated = torch.cuda.memory_allocated(x.device)
+    reusable = max(0, torch.cuda.memory_reserved(x.device) - allocated)
+    headroom = max(0, int(total_bytes * memory_fraction) - allocated)
+    return estimate_batch_chunk_size(
+        batch_size=x.shape[0], seq_len=x.shape[1], d_model=x.shape[2], num_heads=num_heads,
+        element_size=x.element_size(), free_bytes=min(headroom, free_bytes + reusable),
+        total_bytes=total_bytes, score_copies=score_copies, activation_copies=activation_copies,
+        memory_fraction=memory_fraction,
+    )
+
+
+def estimate_batch_chunk_size(*, batch_size: int, seq_len: int, d_model: int, num_heads: int,
+                              element_size: int, free_bytes: int, total_bytes: int, score_copies: int,
+                              activation_copies: int,
+                              memory_fraction: float = DEFAULT_MEMORY_FRACTION) -> int:
+    """Power-of-two chunk from sizes: per item ``act*S*D*e + scores*S^2*H*e`` after reserving the output."""
+    if min(batch_size, seq_len, d_model, num_heads, element_size) <= 0:
+        raise ValueError("tensor dimensions and element_size must be positive")
+    if min(free_bytes, total_bytes) < 0:
+        raise ValueError("memory byte counts must be non-negative")
+    if not 0.0 < memory_fraction <= 1.0:
+        raise ValueError("memory_fraction must be in (0, 1]")
+    if score_copies < 0 or activation_copies <= 0:
+        raise ValueError("memory-copy estimates must be non-negative")
+    allowed = min(free_bytes, int(total_bytes * memory_fraction))
+    working = max(0, allowed - batch_size * seq_len * d_model * element_size)
+    per_item = (activation_copies * seq_len * d_model * element_size
+                + score_copies * seq_len * seq_len * num_heads * element_size)
+    n = max(1, min(batch_size, working // per_item))
+    return 1 << (int(n).bit_length() - 1)
+
+
+def right_padded_lengths(valid_token_mask: torch.Tensor) -> list:
+    """Per-sample prefix lengths as a host list; rejects masks with interior holes."""
+    if valid_token_mask.ndim != 2 or valid_token_mask.dtype != torch.bool:
+        raise ValueError("valid_token_mask must be a two-dimensional bool tensor")
+    lengths = valid_token_mask.sum(dim=1, dtype=torch.int64)
+    pos = torch.arange(valid_token_mask.shape[1], device=valid_token_mask.device)
+    if not bool(torch.equal(valid_token_mask, pos[None, :] < lengths[:, None])):
+        raise ValueError("extreme route requires right-padded prefix masks")
+    return [int(n) for n in lengths.cpu().tolist()]
+
+
+def forward_batch_chunks(forward_chunk: ChunkForward, x: torch.Tensor,
+                         valid_token_mask: Optional[torch.Tensor], chunk_size: int) -> torch.Tensor:
+    """Independent batch slices into one output; an OOM halves the chunk and retries."""
+    if chunk_size <= 0:
+        raise ValueError("chunk_size must be positive")
+    out = torch.empty_like(x)
+    start = 0
+    active = min(chunk_size, x.shape[0])
+    while start < x.shape[0]:
+        end = min(start + active, x.shape[0])
+        mask = None if valid_token_mask is None else valid_token_mask[start:end]
+        try:
+            res = forward_chunk(x[start:end], mask)
+            out[start:end].copy_(res)
+            del res
+            start = end
+        except torch.OutOfMemoryError:
+            if active == 1:
+                raise
+            active = max(1, active // 2)
+            torch.cuda.empty_cache()
+    return out
+
+
+def forward_prefix_chunks(forward_chunk: ChunkForward, x: torch.Tensor,
+                          valid_token_mask: Optional[torch.Tensor], chunk_size: int) -> torch.Tensor:
+    """Equal-length prefix groups, padding trimmed, no mask passed; padded rows stay zero."""
+    lengths = [x.shape[1]] * x.shape[0] if valid_token_mask is None else right_padded_lengths(valid_token_mask)
+    out = torch.zeros_like(x)
+    start = 0
+    active = min(chunk_size, x.shape[0])
+    while start < x.shape[0]:
+        n = lengths[start]
+        end = start + 1
+        while end < x.shape[0] and end - start < active and lengths[end] == n:
+            end += 1
+        if n:
+            try:
+                res = forward_chunk(x[start:end, :n], None)
+                out[start:end, :n].copy_(res)
+                del res
+            except torch.OutOfMemoryError:
+                if active == 1:
+                    raise
+                active = max(1, active // 2)
+                torch.cuda.empty_cache()
+                continue
+        start = end
+    return out
+
+
+class ExactOnlySelfAttention(StridedSDPASelfAttention):
+    """Exact causal attention for trimmed, mask-free extreme-length inputs."""
+
+    def _check(self, x, valid_token_mask):
+        if x.device.type != "cuda":
+            raise RuntimeError("extreme attention requires a ROCm device")
+        if x.dtype not in (torch.float16, torch.float32):
+            raise RuntimeError("extreme attention requires float16 or float32")
+        if valid_token_mask is not None:
+            raise ValueError("trim padding before calling extreme attention")
+
+    def forward(self, x, valid_token_mask=None, causal=False, valid_len=None):
+        self._check(x, valid_token_mask)
+        b, s, _ = x.shape
+        q, k, v = self.project_qkv(x)
+        ctx = scaled_dot_product_attention(q, k, v, is_causal=causal, scale=self.scale)
+        return self.out_proj(ctx.transpose(1, 2).reshape(b, s, self.d_model))
+
+
+class PolyOrExactSelfAttention(ExactOnlySelfAttention):
+    """Extreme-length attention: guarded polynomial route with exact fallback, per head.
+
+    ``route_name(sigma)`` keeps the reference's pure routing predicate for
+    tests; at run time the decision is made per ``(b, h)`` on the device, and
+    ``last_guard`` holds the most recent per-head guard tensors.
+    """
+
+    def __init__(self, d_model: int, num_heads: int) -> None:
+        super().__init__(d_model, num_heads)
+        self.poly_enabled = POLY_ATTENTION_ENABLED
+        self.last_guard = None
+
+    def route_name(self, sigma: Optional[float]) -> str:
+        return "poly" if self.poly_enabled and poly_is_safe(sigma) else "exact"
+
+    def forward(self, x, valid_token_mask=None, causal=False, valid_len=None):
+        self._check(x, valid_token_mask)
+        if not causal:
+            raise ValueError("the polynomial route is causal attention")
+        b, s, _ = x.shape
+        q, k, v = self.project_qkv(x)
+        ctx, self.last_guard = guarded_attention(q, k, v, self.scale, enabled=self.poly_enabled)
+        return self.out_proj(ctx.transpose(1, 2).reshape(b, s, self.d_model))

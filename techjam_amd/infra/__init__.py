@@ -1,0 +1,13 @@
+"""Candidate contract and case tables (mirrors ``src/infra`` of the reference)."""
+
+from .candidate import CandidateSpec, load_candidate, validate_candidate_execution
+from .cases import BENCHMARK_CONFIGS, OfficialCase, load_official_cases
+
+__all__ = [
+    "BENCHMARK_CONFIGS",
+    "CandidateSpec",
+    "OfficialCase",
+    "load_candidate",
+    "load_official_cases",
+    "validate_candidate_execution",
+]

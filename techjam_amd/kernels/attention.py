@@ -153,6 +153,7 @@ class GuardResult:
     """Per-(b,h) outputs of the device-side guard (all device tensors, flattened ``[B*H]``)."""
 
     sigma: torch.Tensor       # float32 [B*H]
+    mean: torch.Tensor        # float32 [B*H]
     smax: torch.Tensor        # float32 [B*H]
     flags: torch.Tensor       # int32   [B*H], 1 = polynomial route
     coeffs: torch.Tensor      # float32 [B*H, 3]
@@ -203,6 +204,7 @@ def score_guard(
     m = b * h
     res = GuardResult(
         sigma=torch.empty(m, dtype=torch.float32, device=dev),
+        mean=torch.empty(m, dtype=torch.float32, device=dev),
         smax=torch.empty(m, dtype=torch.float32, device=dev),
         flags=torch.empty(m, dtype=torch.int32, device=dev),
         coeffs=torch.empty(m, 3, dtype=torch.float32, device=dev),
@@ -213,7 +215,7 @@ def score_guard(
         q.data_ptr(), k.data_ptr(), _DTYPES[q.dtype], b, h, s, d,
         _lib.strides4(q), _lib.strides4(k), float(scale), idx.data_ptr(), idx.numel(),
         float(ceiling), int(exact_prefix),
-        res.sigma.data_ptr(), res.smax.data_ptr(), res.flags.data_ptr(),
+        res.sigma.data_ptr(), res.mean.data_ptr(), res.smax.data_ptr(), res.flags.data_ptr(),
         res.coeffs.data_ptr(), res.row_limit.data_ptr(), res.split.data_ptr(), _stream_ptr(dev),
     )
     _lib.check(code, "tj_score_guard")

@@ -1,0 +1,155 @@
+"""Transformer encoder skeleton whose attention runs on the HIP kernels.
+
+Same module tree, parameter names and construction order as the reference
+model (``torch_transformer_benchmark.py:29-172``), so the harness's strict
+``load_state_dict`` works unchanged and a seeded construction gives the same
+weights. Only the attention module differs: ``HipSelfAttention`` projects with
+``nn.Linear`` (hipBLASLt GEMMs) and calls the gfx950 attention kernel through
+the C ABI instead of materialising a score tensor.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .kernels.attention import scaled_dot_product_attention
+
+
+@dataclass(frozen=True)
+class TransformerConfig:
+    """Static model shape; field names follow ``torch_transformer_benchmark.py:29-56``."""
+
+    batch_size: int
+    seq_len: int
+    d_model: int
+    num_heads: int
+    ffn_dim: int
+    num_layers: int
+    causal: bool
+
+    def validate(self) -> None:
+        for name in ("batch_size", "seq_len", "d_model", "num_heads", "ffn_dim", "num_layers"):
+            if getattr(self, name) <= 0:
+                raise ValueError(f"{name} must be positive")
+        if self.d_model % self.num_heads:
+            raise ValueError(
+                f"d_model ({self.d_model}) must be divisible by num_heads ({self.num_heads})"
+            )
+
+
+def config_key(config) -> tuple:
+    """The 7-tuple route key ``(B, S, d_model, H, ffn, causal, layers)`` (``src/dispatcher.py:74-83``)."""
+    return (config.batch_size, config.seq_len, config.d_model, config.num_heads,
+            config.ffn_dim, config.causal, config.num_layers)
+
+
+class HipSelfAttention(nn.Module):
+    """Multi-head self-attention: Linear projections + the HIP exact kernel.
+
+    ``valid_len`` (int32 ``[B]`` on the device) carries a right-padded mask to
+    the kernel: keys past the length are excluded, padded rows come back as
+    zeros and are zeroed again after the output projection, exactly like the
+    reference (``torch_transformer_benchmark.py:120-121``).
+    """
+
+    def __init__(self, d_model: int, num_heads: int) -> None:
+        super().__init__()
+        if d_model % num_heads:
+            raise ValueError("d_model must be divisible by num_heads")
+        self.d_model = d_model
+        self.num_heads = num_heads
+        self.head_dim = d_model // num_heads
+        self.scale = self.head_dim ** -0.5
+        self.q_proj = nn.Linear(d_model, d_model)
+        self.k_proj = nn.Linear(d_model, d_model)
+        self.v_proj = nn.Linear(d_model, d_model)
+        self.out_proj = nn.Linear(d_model, d_model)
+
+    def heads_view(self, t: torch.Tensor) -> torch.Tensor:
+        """``[B, S, D] -> [B, H, S, dh]`` as a strided view (no copy)."""
+        b, s, _ = t.shape
+        return t.view(b, s, self.num_heads, self.head_dim).transpose(1, 2)
+
+    def project_qkv(self, x: torch.Tensor):
+        return self.heads_view(self.q_proj(x)), self.heads_view(self.k_proj(x)), self.heads_view(self.v_proj(x))
+
+    def attend(self, q, k, v, valid_len, causal):
+        return scaled_dot_product_attention(q, k, v, is_causal=causal, scale=self.scale, valid_len=valid_len)
+
+    def forward(self, x, valid_token_mask=None, causal=False, valid_len=None):
+        b, s, _ = x.shape
+        q, k, v = self.project_qkv(x)
+        ctx = self.attend(q, k, v, valid_len, causal)
+        out = self.out_proj(ctx.transpose(1, 2).reshape(b, s, self.d_model))
+        if valid_token_mask is not None:
+            out = out.masked_fill(~valid_token_mask[..., None], 0)
+        return out
+
+
+class EncoderBlock(nn.Module):
+    """Pre-norm residual block with exact GELU (``torch_transformer_benchmark.py:125-145``)."""
+
+    def __init__(self, d_model: int, num_heads: int, ffn_dim: int) -> None:
+        super().__init__()
+        self.norm1 = nn.LayerNorm(d_model)
+        self.attention = HipSelfAttention(d_model, num_heads)
+        self.norm2 = nn.LayerNorm(d_model)
+        self.ffn_in = nn.Linear(d_model, ffn_dim)
+        self.ffn_out = nn.Linear(ffn_dim, d_model)
+
+    def forward(self, x, valid_token_mask, causal, valid_len=None):
+        x = x + self.attention(self.norm1(x), valid_token_mask, causal, valid_len=valid_len)
+        x = x + self.ffn_out(F.gelu(self.ffn_in(self.norm2(x)), approximate="none"))
+        if valid_token_mask is not None:
+            x = x.masked_fill(~valid_token_mask[..., None], 0)
+        return x
+
+
+class TransformerEncoder(nn.Module):
+    """Layer stack plus final LayerNorm (``torch_transformer_benchmark.py:148-172``)."""
+
+    def __init__(self, config: TransformerConfig) -> None:
+        super().__init__()
+        self.config = config
+        self.layers = nn.ModuleList(
+            EncoderBlock(config.d_model, config.num_heads, config.ffn_dim)
+            for _ in range(config.num_layers)
+        )
+        self.final_norm = nn.LayerNorm(config.d_model)
+
+    def forward_layers(self, x, valid_token_mask=None, valid_len=None):
+        for layer in self.layers:
+            x = layer(x, valid_token_mask, self.config.causal, valid_len=valid_len)
+        x = self.final_norm(x)
+        if valid_token_mask is not None:
+            x = x.masked_fill(~valid_token_mask[..., None], 0)
+        return x
+
+    def forward(self, x, valid_token_mask: Optional[torch.Tensor] = None):
+        valid_len = None if valid_token_mask is None else prefix_lengths(valid_token_mask)
+        return self.forward_layers(x, valid_token_mask, valid_len)
+
+
+def prefix_lengths(valid_token_mask: torch.Tensor) -> torch.Tensor:
+    """Device int32 ``[B]`` valid lengths of a right-padded mask; raises on any other mask.
+
+    One host synchronisation (the prefix check). The dispatcher caches the
+    result per mask tensor so timed loops never pay it.
+    """
+    if valid_token_mask.ndim != 2 or valid_token_mask.dtype != torch.bool:
+        raise ValueError("valid_token_mask must be a two-dimensional bool tensor")
+    lengths = valid_token_mask.sum(dim=1, dtype=torch.int32)
+    pos = torch.arange(valid_token_mask.shape[1], device=valid_token_mask.device)
+    if not bool(torch.equal(valid_token_mask, pos[None, :] < lengths[:, None])):
+        from .errors import UnsupportedCaseError
+
+        raise UnsupportedCaseError(
+            "the HIP attention kernels take right-padded (prefix) masks only; "
+            "left padding or interior gaps are not supported"
+        )
+    return lengths

@@ -88,12 +88,12 @@ def test_guard_rejects_bad_arguments_before_launching():
     st = _strides(64 * 128 * 4, 64, 64 * 4, 1)
     # more samples than rows
     assert L.tj_score_guard(16, 16, _lib.TJ_F32, 1, 4, 128, 64, st, st, 0.125, 16, 256, 0.4, 64,
-                            None, None, 16, None, None, None, None) == _lib.TJ_ERR_SHAPE
+                            None, None, None, 16, None, None, None, None) == _lib.TJ_ERR_SHAPE
     # missing flags output
     assert L.tj_score_guard(16, 16, _lib.TJ_F32, 1, 4, 128, 64, st, st, 0.125, 16, 64, 0.4, 64,
-                            None, None, None, None, None, None, None) == _lib.TJ_ERR_SHAPE
+                            None, None, None, None, None, None, None, None) == _lib.TJ_ERR_SHAPE
     assert L.tj_score_guard(16, 16, _lib.TJ_F32, 1, 4, 128, 256, st, st, 0.125, 16, 64, 0.4, 64,
-                            None, None, 16, None, None, None, None) == _lib.TJ_ERR_UNSUPPORTED
+                            None, None, None, 16, None, None, None, None) == _lib.TJ_ERR_UNSUPPORTED
 
 
 def test_check_maps_codes_to_reference_exceptions():
