@@ -1,11 +1,613 @@
-// Polynomial linear attention (placeholder until the kernels land).
+// Chunked causal degree-2 polynomial linear attention for gfx950 (D = 64, chunk 512).
+//
+// Replaces the reference's chunk scan (src/implementations/poly_reference.py:162-249)
+// and its Triton kernels quad_apply / quad_update / causal_diag
+// (src/kernels/poly_attention_triton.py:151-257, :420-591). With a = q*sqrt(scale),
+// b = k*sqrt(scale) (fp16) and per-head coefficients (c0, c1, c2), chunk
+// [t0, t1) emits for each row i
+//   num = c0*S_const + c1*a.S_lin + c2*phi2(a).S_quad + sum_{t0<=j<=i} exp(a_i.b_j) v_j
+//   den = c0*t0      + c1*a.z    + c2*a^T G a        + sum_{t0<=j<=i} exp(a_i.b_j)
+// and the states fold in the chunk afterwards:
+//   S_quad[(i,j), v] += sum_t b_ti b_tj v_tv,  S_lin[j, v] += sum_t b_tj v_tv,
+//   G[i, j] += sum_t b_ti b_tj,  z[j] += sum_t b_tj,  S_const[v] += sum_t v_tv.
+//
+// One launch per chunk; every head owns 13 workgroups with three roles:
+//   * apply (4 per head, 128 rows each): quadratic term as
+//       y^T = sum_i S_i^T (a_i * a^T)  (S_i = rows (i, .) of S_quad),
+//     i.e. 64 MFMA GEMMs whose B operand is the fp16 product a_i*a_j built in
+//     registers -- phi2(a) never exists in memory; linear and denominator terms
+//     as three more small GEMMs; the exact diagonal block like the exact
+//     kernel (S^T = b a^T in registers, no max subtraction).
+//   * quad update (8 per head, 8 i-slices each): S_i += (b_i * b)^T v over the
+//     chunk's tokens, accumulated straight into MFMA accumulators that hold the
+//     fp32 master in its register image (the master's memory layout IS the
+//     accumulator layout, so loading and storing it is straight 16-byte copies).
+//     It also writes the fp16 shadow the next chunk's apply reads.
+//   * small-state update (1 per head): S_lin, G, z, S_const.
+// Apply reads state shadow [c & 1] (the state before chunk c) while the update
+// writes shadow [(c + 1) & 1], so both roles of a chunk run in the same launch.
+// Heads whose guard flag is 0 exit at once (the exact kernel covers them).
 #include "tj_common.h"
 
-extern "C" size_t tj_poly_workspace_bytes(int64_t, int64_t, int64_t, int64_t, int64_t) { return 0; }
+namespace tj {
+namespace {
 
-extern "C" int tj_poly_attn_fwd(const void*, const void*, const void*, void*, int, int64_t, int64_t,
-                                int64_t, int64_t, const int64_t*, const int64_t*, const int64_t*,
-                                const int64_t*, float, int64_t, int64_t, const float*, const int32_t*,
-                                void*, size_t, hipStream_t) {
-  return TJ_ERR_UNSUPPORTED;
+constexpr int PD = 64;         // head dim (d = dv)
+constexpr int PC = 512;        // chunk length
+constexpr int PT = 256;        // threads per workgroup
+constexpr int NAPPLY = 4;      // apply workgroups per head (128 rows each)
+constexpr int NUPD = 8;        // quad-update workgroups per head (8 i-slices each)
+constexpr int NROLE = NAPPLY + NUPD + 1;
+constexpr int LP = 72;         // padded LDS row of 64 halves (144 bytes)
+constexpr int AP = 66;         // padded LDS row of the a tile (132 bytes, conflict-free u16 reads)
+
+// Workspace of one head (byte offsets).
+constexpr size_t kQuadImg = 0;                                   // fp32 [64 i][2 jb][2 vb][64 lanes][16]
+constexpr size_t kQuadImgBytes = size_t(PD) * 4 * 64 * 16 * 4;  // 1 MiB
+constexpr size_t kLinImg = kQuadImg + kQuadImgBytes;             // fp32 [2 jb][2 vb][64][16]
+constexpr size_t kGramImg = kLinImg + 4 * 64 * 16 * 4;           // fp32 [2 ib][2 jb][64][16]
+constexpr size_t kZsMaster = kGramImg + 4 * 64 * 16 * 4;         // fp32 z[64], S_const[64]
+constexpr size_t kQuadShadow = kZsMaster + 128 * 4;              // fp16 [2][64 i][64 v][64 j]
+constexpr size_t kLinShadow = kQuadShadow + 2 * size_t(PD) * PD * PD * 2;  // fp16 [2][64 v][64 j]
+constexpr size_t kGramShadow = kLinShadow + 2 * PD * PD * 2;     // fp16 [2][64][64] (symmetric)
+constexpr size_t kZsShadow = kGramShadow + 2 * PD * PD * 2;      // fp32 [2][128]
+constexpr size_t kPerHead = (kZsShadow + 2 * 128 * 4 + 255) & ~size_t(255);
+
+// LDS: apply = quad staging / diagonal tiles (36864) + a tile (16896);
+//      updates = two transposed token tiles, double buffered (36864).
+constexpr int kStageBytes = 4 * 64 * LP * 2;
+constexpr int kATileBytes = 128 * AP * 2;
+constexpr int kSmemBytes = kStageBytes + kATileBytes;
+
+struct PolyArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  View4 vq, vk, vv, vo;
+  int H, S;
+  float rs;             // sqrt(scale)
+  int t0, t1;           // chunk rows
+  int prefix_end;       // rows below are left to the exact kernel
+  int emit, update;     // roles active in this launch
+  int cur;              // shadow slot holding the state before this chunk
+  const float* coeffs;  // [M][3]
+  const int32_t* flags; // [M] or null
+  char* ws;
+  int total;            // M * NROLE
+  int per_xcd;
+};
+
+__device__ __forceinline__ float4_t ld4(const float* p) { return *reinterpret_cast<const float4_t*>(p); }
+
+template <typename T>
+__device__ __forceinline__ void load_row4(const T* p, float out[4]) {
+  if constexpr (sizeof(T) == 4) {
+    const float4_t x = *reinterpret_cast<const float4_t*>(p);
+    out[0] = x[0]; out[1] = x[1]; out[2] = x[2]; out[3] = x[3];
+  } else {
+    const half4_t x = *reinterpret_cast<const half4_t*>(p);
+    out[0] = (float)x[0]; out[1] = (float)x[1]; out[2] = (float)x[2]; out[3] = (float)x[3];
+  }
+}
+
+// Global -> registers of one 64-token x 64-dim tile of k (scaled by rs) and v.
+// Unit = (4-token group g, 4-dim group c); one unit per thread.
+template <typename T>
+struct TokTile {
+  float kx[4][4];
+  float vx[4][4];
+  __device__ __forceinline__ static void coords(int tid, int& g, int& c) {
+    g = (tid >> 2) & 15;
+    c = (tid & 3) | ((tid >> 6) << 2);
+  }
+  __device__ __forceinline__ void load(const PolyArgs& a, int b, int h, int tok0, int tok_end, int tid) {
+    int g, c;
+    coords(tid, g, c);
+    const T* kp = reinterpret_cast<const T*>(a.k);
+    const T* vp = reinterpret_cast<const T*>(a.v);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = tok0 + 4 * g + r;
+      if (t < tok_end) {
+        load_row4<T>(kp + a.vk.row(b, h, t) + 4 * c, kx[r]);
+        load_row4<T>(vp + a.vv.row(b, h, t) + 4 * c, vx[r]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) kx[r][e] *= a.rs;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) kx[r][e] = vx[r][e] = 0.f;
+      }
+    }
+  }
+  // Both transposed ([dim][token], token order as given): the update roles.
+  __device__ __forceinline__ void store_transposed(half_t (*bt)[LP], half_t (*vt)[LP], int tid) const {
+    int g, c;
+    coords(tid, g, c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      half4_t hb = {(half_t)kx[0][e], (half_t)kx[1][e], (half_t)kx[2][e], (half_t)kx[3][e]};
+      half4_t hv = {(half_t)vx[0][e], (half_t)vx[1][e], (half_t)vx[2][e], (half_t)vx[3][e]};
+      *reinterpret_cast<half4_t*>(&bt[4 * c + e][4 * g]) = hb;
+      *reinterpret_cast<half4_t*>(&vt[4 * c + e][4 * g]) = hv;
+    }
+  }
+  // K row-major, V transposed in key_slot order: the diagonal block (as in the exact kernel).
+  __device__ __forceinline__ void store_diag(half_t (*kb)[LP], half_t (*vt)[LP], int tid) const {
+    int g, c;
+    coords(tid, g, c);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      half4_t hk = {(half_t)kx[r][0], (half_t)kx[r][1], (half_t)kx[r][2], (half_t)kx[r][3]};
+      *reinterpret_cast<half4_t*>(&kb[4 * g + r][4 * c]) = hk;
+    }
+    const int slot = key_slot(4 * g);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      half4_t hv = {(half_t)vx[0][e], (half_t)vx[1][e], (half_t)vx[2][e], (half_t)vx[3][e]};
+      *reinterpret_cast<half4_t*>(&vt[4 * c + e][slot]) = hv;
+    }
+  }
+};
+
+__device__ __forceinline__ half8_t mul8(half8_t x, half_t s) {
+  half8_t r;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = x[j] * s;
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// Apply role: rows [row0, row0 + 128) of the chunk.
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int m, int qt, char* smem) {
+  const int row0 = a.t0 + 128 * qt;
+  if (row0 >= a.t1 || row0 + 128 <= a.prefix_end) return;
+  auto sst = reinterpret_cast<half_t(*)[64][LP]>(smem);                 // [4][64][LP]
+  auto kb = reinterpret_cast<half_t(*)[64][LP]>(smem);                  // diag: [2][64][LP]
+  auto vt = reinterpret_cast<half_t(*)[64][LP]>(smem + 2 * 64 * LP * 2);  // diag: [2][64][LP]
+  auto at = reinterpret_cast<half_t(*)[AP]>(smem + kStageBytes);       // [128][AP]
+
+  const int tid = threadIdx.x, w = tid / kWave, lane = tid % kWave, hl = lane / 32, ln = lane % 32;
+  const int qw0 = row0 + 32 * w;
+  const int qi = qw0 + ln;
+  const int qrow = 32 * w + ln;
+
+  // a = fp16(q * rs); B operand slots (hl, j) <-> dim 16*ks + 8*hl + j.
+  half8_t aB[4];
+  {
+    const T* qp = reinterpret_cast<const T*>(a.q);
+    const bool in = qi < a.t1;
+    const int64_t base = a.vq.row(b, h, in ? qi : a.t0);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      float x[8];
+      load_row4<T>(qp + base + 16 * ks + 8 * hl, x);
+      load_row4<T>(qp + base + 16 * ks + 8 * hl + 4, x + 4);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) aB[ks][j] = in ? (half_t)(x[j] * a.rs) : (half_t)0.f;
+      // AP rows are only 4-byte aligned: store as four half2.
+#pragma unroll
+      for (int j = 0; j < 8; j += 2)
+        *reinterpret_cast<half2_t*>(&at[qrow][16 * ks + 8 * hl + j]) = half2_t{aB[ks][j], aB[ks][j + 1]};
+    }
+  }
+
+  const half_t* qshadow = reinterpret_cast<const half_t*>(ws + kQuadShadow) + size_t(a.cur) * PD * PD * PD;
+  // Stage the shadow rows of two i (2 x 64 x 64 fp16) into LDS buffer `buf`.
+  auto stage = [&](int pair, int buf) {
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int e = tid + it * PT;          // 1024 16-byte pieces
+      const int ii = e >> 9, rem = e & 511;
+      const int vrow = rem >> 3, piece = rem & 7;
+      const half8_t x = *reinterpret_cast<const half8_t*>(qshadow + (size_t(2 * pair + ii) * PD + vrow) * PD + 8 * piece);
+      *reinterpret_cast<half8_t*>(&sst[2 * buf + ii][vrow][8 * piece]) = x;
+    }
+  };
+
+  float16_t accq[2];
+#pragma unroll
+  for (int vb = 0; vb < 2; ++vb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) accq[vb][r] = 0.f;
+
+  stage(0, 0);
+  __syncthreads();
+  for (int p = 0; p < PD / 2; ++p) {
+    const int buf = p & 1;
+    if (p + 1 < PD / 2) stage(p + 1, buf ^ 1);
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+      const half_t ai = at[qrow][2 * p + ii];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const half8_t bop = mul8(aB[ks], ai);
+#pragma unroll
+        for (int vb = 0; vb < 2; ++vb) {
+          const half8_t sa = *reinterpret_cast<const half8_t*>(&sst[2 * buf + ii][32 * vb + ln][16 * ks + 8 * hl]);
+          accq[vb] = mfma32(sa, bop, accq[vb]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  // Linear numerator term S_lin^T a^T and the quadratic denominator G a^T
+  // (operands straight from the L2-resident shadows).
+  const half_t* lsh = reinterpret_cast<const half_t*>(ws + kLinShadow) + size_t(a.cur) * PD * PD;
+  const half_t* gsh = reinterpret_cast<const half_t*>(ws + kGramShadow) + size_t(a.cur) * PD * PD;
+  const float* zs = reinterpret_cast<const float*>(ws + kZsShadow) + a.cur * 128;
+  float16_t accl[2], ug[2];
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) accl[blk][r] = ug[blk][r] = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+      const half8_t la = *reinterpret_cast<const half8_t*>(lsh + (32 * blk + ln) * PD + 16 * ks + 8 * hl);
+      const half8_t ga = *reinterpret_cast<const half8_t*>(gsh + (32 * blk + ln) * PD + 16 * ks + 8 * hl);
+      accl[blk] = mfma32(la, aB[ks], accl[blk]);
+      ug[blk] = mfma32(ga, aB[ks], ug[blk]);
+    }
+  // a^T G a: rows i of ug pair with a_i from the a tile; a.z over this lane's 32 dims.
+  float den_q = 0.f, den_l = 0.f;
+#pragma unroll
+  for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int i = 32 * blk + 8 * (r / 4) + 4 * hl + (r % 4);
+      den_q += (float)at[qrow][i] * ug[blk][r];
+    }
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) den_l += (float)aB[ks][j] * zs[16 * ks + 8 * hl + j];
+  den_q += xor32(den_q);
+  den_l += xor32(den_l);
+
+  // Exact diagonal block: keys [t0, min(t1, row0 + 128)), no max subtraction.
+  float16_t accd[2];
+#pragma unroll
+  for (int vb = 0; vb < 2; ++vb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) accd[vb][r] = 0.f;
+  float den_d = 0.f;
+  const int key_end = min(a.t1, row0 + 128);
+  const int n_kt = (key_end - a.t0 + 63) / 64;
+  const int wave_last = min(qw0 + 31, key_end - 1);
+  TokTile<T> tile;
+  tile.load(a, b, h, a.t0, key_end, tid);
+  tile.store_diag(kb[0], vt[0], tid);
+  __syncthreads();
+  for (int kt = 0; kt < n_kt; ++kt) {
+    const int cur = kt & 1;
+    const int kv0 = a.t0 + 64 * kt;
+    if (kt + 1 < n_kt) tile.load(a, b, h, kv0 + 64, key_end, tid);
+    if (kv0 <= wave_last) {
+      float16_t s[2];
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[kh][r] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const half8_t kf = *reinterpret_cast<const half8_t*>(&kb[cur][32 * kh + ln][16 * ks + 8 * hl]);
+          s[kh] = mfma32(kf, aB[ks], s[kh]);
+        }
+      }
+      half8_t pf[4];
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kv0 + 32 * kh + 8 * (r / 4) + 4 * hl + (r % 4);
+          const float wgt = key <= qi ? fast_exp2(s[kh][r] * 1.4426950408889634f) : 0.f;
+          const half_t wh = (half_t)wgt;
+          den_d += (float)wh;
+          pf[2 * kh + r / 8][r % 8] = wh;
+        }
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int vb = 0; vb < 2; ++vb) {
+          const half8_t vf = *reinterpret_cast<const half8_t*>(&vt[cur][32 * vb + ln][16 * st + 8 * hl]);
+          accd[vb] = mfma32(vf, pf[st], accd[vb]);
+        }
+    }
+    if (kt + 1 < n_kt) tile.store_diag(kb[cur ^ 1], vt[cur ^ 1], tid);
+    __syncthreads();
+  }
+  den_d += xor32(den_d);
+
+  if (qi >= a.t1 || qi < a.prefix_end) return;
+  const float c0 = a.coeffs[3 * m], c1 = a.coeffs[3 * m + 1], c2 = a.coeffs[3 * m + 2];
+  const float den = c0 * (float)a.t0 + c1 * den_l + c2 * den_q + den_d;
+  const float inv = 1.f / den;
+  T* op = reinterpret_cast<T*>(a.o) + a.vo.row(b, h, qi);
+#pragma unroll
+  for (int vb = 0; vb < 2; ++vb)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int v0 = 32 * vb + 8 * g + 4 * hl;
+      const float4_t sc = ld4(zs + 64 + v0);
+      float y[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        y[e] = (c0 * sc[e] + c1 * accl[vb][4 * g + e] + c2 * accq[vb][4 * g + e] + accd[vb][4 * g + e]) * inv;
+      if constexpr (sizeof(T) == 4) {
+        *reinterpret_cast<float4_t*>(op + v0) = float4_t{y[0], y[1], y[2], y[3]};
+      } else {
+        *reinterpret_cast<half4_t*>(op + v0) = half4_t{(half_t)y[0], (half_t)y[1], (half_t)y[2], (half_t)y[3]};
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Update roles: fold the chunk's tokens into the states.
+// ---------------------------------------------------------------------------
+
+// Streams the chunk's tokens through LDS as transposed fp16 tiles and calls
+// body(bt, vt, tok) for every 16-token MFMA k-step.
+template <typename T, typename Body>
+__device__ __forceinline__ void stream_tokens(const PolyArgs& a, int b, int h, char* smem, Body&& body) {
+  auto bt = reinterpret_cast<half_t(*)[64][LP]>(smem);
+  auto vt = reinterpret_cast<half_t(*)[64][LP]>(smem + 2 * 64 * LP * 2);
+  const int tid = threadIdx.x;
+  const int n_blk = (a.t1 - a.t0 + 63) / 64;
+  TokTile<T> tile;
+  tile.load(a, b, h, a.t0, a.t1, tid);
+  tile.store_transposed(bt[0], vt[0], tid);
+  __syncthreads();
+  for (int blk = 0; blk < n_blk; ++blk) {
+    const int cur = blk & 1;
+    if (blk + 1 < n_blk) tile.load(a, b, h, a.t0 + 64 * (blk + 1), a.t1, tid);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) body(bt[cur], vt[cur], 16 * ks);
+    if (blk + 1 < n_blk) tile.store_transposed(bt[cur ^ 1], vt[cur ^ 1], tid);
+    __syncthreads();
+  }
+}
+
+__device__ __forceinline__ void load_img(const float* img, float16_t& acc) {
+  const int lane = threadIdx.x % kWave;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float4_t x = ld4(img + lane * 16 + 4 * q);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[4 * q + e] = x[e];
+  }
+}
+
+__device__ __forceinline__ void store_img(float* img, const float16_t& acc) {
+  const int lane = threadIdx.x % kWave;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    *reinterpret_cast<float4_t*>(img + lane * 16 + 4 * q) = float4_t{acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]};
+}
+
+// acc holds D[row][col] of a 32x32 block (rows 32*rb + ..., column 32*cb + ln);
+// writes it transposed as fp16 into dst[col][row] (row-contiguous, 4 rows per store).
+__device__ __forceinline__ void store_shadow_t(half_t* dst, const float16_t& acc, int rb, int cb) {
+  const int lane = threadIdx.x % kWave, hl = lane / 32, ln = lane % 32;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int row = 32 * rb + 8 * g + 4 * hl;
+    *reinterpret_cast<half4_t*>(dst + (32 * cb + ln) * PD + row) =
+        half4_t{(half_t)acc[4 * g], (half_t)acc[4 * g + 1], (half_t)acc[4 * g + 2], (half_t)acc[4 * g + 3]};
+  }
+}
+
+template <typename T>
+__device__ void quad_update_role(const PolyArgs& a, char* ws, int b, int h, int ug, char* smem) {
+  const int w = threadIdx.x / kWave, lane = threadIdx.x % kWave, hl = lane / 32, ln = lane % 32;
+  const int i0 = 8 * ug + 2 * w;  // this wave's two i-slices
+  float* img = reinterpret_cast<float*>(ws + kQuadImg);
+  // acc[ii][jb][vb] = D[j][v] block of S_i (rows j, columns v).
+  float16_t acc[2][2][2];
+#pragma unroll
+  for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+      for (int vb = 0; vb < 2; ++vb) load_img(img + ((size_t(i0 + ii) * 2 + jb) * 2 + vb) * 1024, acc[ii][jb][vb]);
+
+  stream_tokens<T>(a, b, h, smem, [&](half_t (*bt)[LP], half_t (*vt)[LP], int tk) {
+    const int t = tk + 8 * hl;
+    half8_t bj[2], vv[2];
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      bj[x] = *reinterpret_cast<const half8_t*>(&bt[32 * x + ln][t]);
+      vv[x] = *reinterpret_cast<const half8_t*>(&vt[32 * x + ln][t]);
+    }
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+      const half8_t bi = *reinterpret_cast<const half8_t*>(&bt[i0 + ii][t]);
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) {
+        half8_t phi;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) phi[j] = bj[jb][j] * bi[j];
+#pragma unroll
+        for (int vb = 0; vb < 2; ++vb) acc[ii][jb][vb] = mfma32(phi, vv[vb], acc[ii][jb][vb]);
+      }
+    }
+  });
+
+  half_t* sh = reinterpret_cast<half_t*>(ws + kQuadShadow) + size_t(a.cur ^ 1) * PD * PD * PD;
+#pragma unroll
+  for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+      for (int vb = 0; vb < 2; ++vb) {
+        store_img(img + ((size_t(i0 + ii) * 2 + jb) * 2 + vb) * 1024, acc[ii][jb][vb]);
+        store_shadow_t(sh + size_t(i0 + ii) * PD * PD, acc[ii][jb][vb], jb, vb);
+      }
+}
+
+template <typename T>
+__device__ void small_update_role(const PolyArgs& a, char* ws, int b, int h, char* smem) {
+  const int w = threadIdx.x / kWave, lane = threadIdx.x % kWave, hl = lane / 32, ln = lane % 32;
+  float* lin_img = reinterpret_cast<float*>(ws + kLinImg);
+  float* gram_img = reinterpret_cast<float*>(ws + kGramImg);
+  float* zs = reinterpret_cast<float*>(ws + kZsMaster);
+  float16_t acc[2][2];
+  if (w < 2) {
+    float* img = w == 0 ? lin_img : gram_img;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) load_img(img + (rb * 2 + cb) * 1024, acc[rb][cb]);
+  }
+  float zsum = 0.f, csum = 0.f;
+  stream_tokens<T>(a, b, h, smem, [&](half_t (*bt)[LP], half_t (*vt)[LP], int tk) {
+    const int t = tk + 8 * hl;
+    if (w == 0) {  // S_lin[j][v] = sum_t b_tj v_tv
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) {
+        const half8_t bj = *reinterpret_cast<const half8_t*>(&bt[32 * jb + ln][t]);
+#pragma unroll
+        for (int vb = 0; vb < 2; ++vb)
+          acc[jb][vb] = mfma32(bj, *reinterpret_cast<const half8_t*>(&vt[32 * vb + ln][t]), acc[jb][vb]);
+      }
+    } else if (w == 1) {  // G[i][j] = sum_t b_ti b_tj
+#pragma unroll
+      for (int ib = 0; ib < 2; ++ib) {
+        const half8_t bi = *reinterpret_cast<const half8_t*>(&bt[32 * ib + ln][t]);
+#pragma unroll
+        for (int jb = 0; jb < 2; ++jb)
+          acc[ib][jb] = mfma32(bi, *reinterpret_cast<const half8_t*>(&bt[32 * jb + ln][t]), acc[ib][jb]);
+      }
+    } else if (w == 2) {  // z[d] and S_const[d]: lane = dim, 16 tokens per step
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        zsum += (float)bt[lane][tk + j];
+        csum += (float)vt[lane][tk + j];
+      }
+    }
+  });
+
+  const int nxt = a.cur ^ 1;
+  if (w == 0) {
+    half_t* sh = reinterpret_cast<half_t*>(ws + kLinShadow) + size_t(nxt) * PD * PD;  // [v][j]
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+      for (int vb = 0; vb < 2; ++vb) {
+        store_img(lin_img + (jb * 2 + vb) * 1024, acc[jb][vb]);
+        store_shadow_t(sh, acc[jb][vb], jb, vb);
+      }
+  } else if (w == 1) {
+    half_t* sh = reinterpret_cast<half_t*>(ws + kGramShadow) + size_t(nxt) * PD * PD;  // symmetric
+#pragma unroll
+    for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) {
+        store_img(gram_img + (ib * 2 + jb) * 1024, acc[ib][jb]);
+        store_shadow_t(sh, acc[ib][jb], ib, jb);
+      }
+  } else if (w == 2) {
+    const float z = zs[lane] + zsum;
+    const float c = zs[64 + lane] + csum;
+    zs[lane] = z;
+    zs[64 + lane] = c;
+    float* zsh = reinterpret_cast<float*>(ws + kZsShadow) + nxt * 128;
+    zsh[lane] = z;
+    zsh[64 + lane] = c;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(PT, 2) void poly_chunk_kernel(PolyArgs a) {
+  __shared__ __attribute__((aligned(16))) char smem[kSmemBytes];
+  const int id = blockIdx.x;
+  const int logical = (id % kNumXcd) * a.per_xcd + id / kNumXcd;
+  if (logical >= a.total) return;
+  const int m = logical / NROLE;
+  const int role = logical % NROLE;
+  if (a.flags != nullptr && a.flags[m] == 0) return;
+  const int b = m / a.H, h = m % a.H;
+  char* ws = a.ws + size_t(m) * kPerHead;
+  if (role < NAPPLY) {
+    if (a.emit) apply_role<T>(a, ws, b, h, m, role, smem);
+  } else if (role < NAPPLY + NUPD) {
+    if (a.update) quad_update_role<T>(a, ws, b, h, role - NAPPLY, smem);
+  } else {
+    if (a.update) small_update_role<T>(a, ws, b, h, smem);
+  }
+}
+
+__global__ void zero_kernel(float4_t* p, size_t n) {
+  for (size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
+    p[i] = float4_t{0.f, 0.f, 0.f, 0.f};
+}
+
+template <typename T>
+int run(PolyArgs a, int S, int chunk, size_t ws_bytes, hipStream_t stream) {
+  hipLaunchKernelGGL(zero_kernel, dim3(1024), dim3(256), 0, stream, reinterpret_cast<float4_t*>(a.ws),
+                     ws_bytes / 16);
+  if (hipGetLastError() != hipSuccess) return TJ_ERR_LAUNCH;
+  const int n_chunks = (S + chunk - 1) / chunk;
+  for (int c = 0; c < n_chunks; ++c) {
+    a.t0 = c * chunk;
+    a.t1 = min(S, a.t0 + chunk);
+    a.emit = a.t1 > a.prefix_end ? 1 : 0;
+    a.update = c + 1 < n_chunks ? 1 : 0;
+    a.cur = c & 1;
+    if (!a.emit && !a.update) continue;
+    hipLaunchKernelGGL(poly_chunk_kernel<T>, dim3(a.per_xcd * kNumXcd), dim3(PT), 0, stream, a);
+    if (hipGetLastError() != hipSuccess) return TJ_ERR_LAUNCH;
+  }
+  return TJ_OK;
+}
+
+}  // namespace
+}  // namespace tj
+
+extern "C" size_t tj_poly_workspace_bytes(int64_t B, int64_t H, int64_t S, int64_t D, int64_t chunk) {
+  (void)S;
+  (void)chunk;
+  if (B <= 0 || H <= 0 || D != tj::PD) return 0;
+  return size_t(B * H) * tj::kPerHead;
+}
+
+extern "C" int tj_poly_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype,
+                                int64_t B, int64_t H, int64_t S, int64_t D,
+                                const int64_t q_strides[4], const int64_t k_strides[4],
+                                const int64_t v_strides[4], const int64_t o_strides[4],
+                                float scale, int64_t chunk, int64_t exact_prefix,
+                                const float* coeffs, const int32_t* flags,
+                                void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (dtype != TJ_F32 && dtype != TJ_F16) return TJ_ERR_DTYPE;
+  if (B < 0 || H <= 0 || S < 0 || D <= 0 || chunk <= 0 || exact_prefix < 0 || !(scale > 0.f)) return TJ_ERR_SHAPE;
+  if (D != tj::PD || chunk != tj::PC) return TJ_ERR_UNSUPPORTED;
+  if (B == 0 || S == 0 || exact_prefix >= S) return TJ_OK;
+  if (B * H * tj::NROLE >= (int64_t(1) << 31) || S >= (int64_t(1) << 30)) return TJ_ERR_SHAPE;
+  if (!q || !k || !v || !o || !coeffs) return TJ_ERR_SHAPE;
+  if (!tjh::view_ok(q, q_strides, dtype) || !tjh::view_ok(k, k_strides, dtype) ||
+      !tjh::view_ok(v, v_strides, dtype) || !tjh::view_ok(o, o_strides, dtype))
+    return TJ_ERR_ALIGN;
+  const size_t need = size_t(B * H) * tj::kPerHead;
+  if (workspace == nullptr || workspace_bytes < need || !tjh::aligned16(workspace)) return TJ_ERR_WORKSPACE;
+
+  tj::PolyArgs a;
+  a.q = q; a.k = k; a.v = v; a.o = o;
+  a.vq = {q_strides[0], q_strides[1], q_strides[2]};
+  a.vk = {k_strides[0], k_strides[1], k_strides[2]};
+  a.vv = {v_strides[0], v_strides[1], v_strides[2]};
+  a.vo = {o_strides[0], o_strides[1], o_strides[2]};
+  a.H = (int)H; a.S = (int)S;
+  a.rs = sqrtf(scale);
+  a.prefix_end = (int)exact_prefix;
+  a.coeffs = coeffs;
+  a.flags = flags;
+  a.ws = static_cast<char*>(workspace);
+  a.total = (int)(B * H) * tj::NROLE;
+  a.per_xcd = (a.total + tj::kNumXcd - 1) / tj::kNumXcd;
+  if (dtype == TJ_F32) return tj::run<float>(a, (int)S, (int)chunk, need, stream);
+  return tj::run<half_t>(a, (int)S, (int)chunk, need, stream);
 }
