@@ -45,7 +45,8 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--workload", default="attn-core", choices=["attn-core", "copy-1gib"])
+    p.add_argument("--workload", default="attn-core",
+                   choices=["attn-core", "extreme", "model-c1", "model-c2", "model-c4", "copy-1gib"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-repeats", type=int, default=3)
     return p.parse_args()
@@ -96,6 +97,69 @@ def copy_1gib(args, dev):
     return step, n, 0.0, 2.0 * 4 * n, config, "copy_1gib_calibration.md"
 
 
+def extreme(args, dev):
+    """Guarded polynomial attention, B=4 S=65536 H=16 D=64; head 0 of each sample at sigma 4."""
+    from oracle.poly import poly_flops
+    from techjam_amd.implementations.poly_attention import guarded_attention
+
+    b, s, h, d = 4, 65536, 16, 64
+    g = torch.Generator(device=dev).manual_seed(1234 + 100000)
+    q = torch.randn(b, s, h, d, generator=g, device=dev) * 0.5
+    k = torch.randn(b, s, h, d, generator=g, device=dev) * 0.5
+    v = torch.randn(b, s, h, d, generator=g, device=dev)
+    q[:, :, 0] = torch.randn(b, s, d, generator=g, device=dev) * 2.0
+    k[:, :, 0] = torch.randn(b, s, d, generator=g, device=dev) * 2.0
+    qh, kh, vh = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+    out = torch.empty(b, s, h, d, device=dev).transpose(1, 2)
+    scale = d ** -0.5
+
+    def step():
+        guarded_attention(qh, kh, vh, scale, out=out)
+
+    n_poly, n_exact = b * (h - 1), b
+    flops = n_poly * poly_flops(s, d, d, 512, 4096) + n_exact * 2.0 * d * s * (s + 1)
+    bytes_alg = 16.0 * b * s * h * d
+    config = {
+        "workload": "extreme-length attention core: guarded degree-2 polynomial attention, "
+                    "B=4 S=65536 H=16 D=64, fp32 io, 60 polynomial heads + 4 exact fallback heads",
+        "batch": b, "seq_len": s, "heads": h, "head_dim": d, "chunk": 512, "exact_prefix": 4096,
+    }
+    return step, b * s, flops, bytes_alg, config, "poly_extreme_b4_s65536_h16_d64.md"
+
+
+def model(name):
+    def build(args, dev):
+        from oracle.model import DenseTransformer, generate_random_case
+        from oracle.model import TransformerConfig as OracleConfig
+        from techjam_amd.dispatcher import DispatchingTransformer
+        from techjam_amd.infra import BENCHMARK_CONFIGS
+
+        c = BENCHMARK_CONFIGS[name]
+        cfg = OracleConfig(c.batch_size, c.seq_len, c.d_model, c.num_heads, c.ffn_dim, c.num_layers, c.causal)
+        torch.manual_seed(1234)
+        base = DenseTransformer(cfg).eval()
+        cand = DispatchingTransformer(cfg).eval()
+        cand.load_state_dict(base.state_dict())
+        cand = cand.to(dev)
+        x, mask = generate_random_case(cfg, torch.device("cpu"), torch.float32, 1234 + 100000,
+                                       c.padding_ratio, 1.0)
+        x, mask = x.to(dev), mask.to(dev)
+        lengths = mask.sum(1).tolist()
+
+        def step():
+            with torch.inference_mode():
+                cand(x, mask)
+
+        hd = c.d_model // c.num_heads
+        flops = c.num_layers * 2.0 * hd * c.num_heads * sum(n * (n + 1) for n in lengths)
+        config = {"workload": f"{c.num_layers}-layer encoder {name}: {c.description}",
+                  "batch": c.batch_size, "seq_len": c.seq_len, "d_model": c.d_model,
+                  "heads": c.num_heads, "ffn_dim": c.ffn_dim, "layers": c.num_layers,
+                  "roofline_scope": "attention FLOPs over the whole forward (GEMMs not counted)"}
+        return step, c.batch_size * c.seq_len, flops, 0.0, config, f"model_{name.lower()}.md"
+    return build
+
+
 def cpu_baseline_attn_core(repeats: int):
     """Dense FP32 oracle attention on the host: one batch element (16 heads x 4096)."""
     from oracle.model import DenseSelfAttention
@@ -136,11 +200,11 @@ def main():
     dev = torch.device("cuda:0")
     torch.backends.cuda.matmul.allow_tf32 = False
 
-    if args.workload == "copy-1gib":
-        step, tokens, flops, bytes_alg, config, prof_name = copy_1gib(args, dev)
+    builders = {"attn-core": attn_core, "extreme": extreme, "copy-1gib": copy_1gib,
+                "model-c1": model("C1"), "model-c2": model("C2"), "model-c4": model("C4")}
+    step, tokens, flops, bytes_alg, config, prof_name = builders[args.workload](args, dev)
+    if args.workload != "attn-core":
         args.no_cpu_baseline = True
-    else:
-        step, tokens, flops, bytes_alg, config, prof_name = attn_core(args, dev)
 
     for _ in range(args.warmup):
         step()
