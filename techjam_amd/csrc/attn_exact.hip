@@ -32,10 +32,10 @@
 namespace tj {
 namespace {
 
-constexpr int BM = 128;    // query rows per workgroup
 constexpr int BN = 64;     // keys per tile
 constexpr int NT = 256;    // threads per workgroup
 constexpr int PAD = 8;     // fp16 padding per LDS row (16 bytes)
+constexpr float kRescaleLog2 = 8.f;  // lazy-rescale threshold of the running max (log2 units)
 
 struct AttnArgs {
   const void* q;
@@ -153,58 +153,69 @@ struct KVStage {
   }
 };
 
-// One query tile of one (b, h). SPLIT selects the three-MFMA score path.
-template <typename T, int HD, bool SPLIT, typename SM>
+// One query tile of one (b, h): 4 waves x 32*QB rows. Each wave holds QB
+// 32-row query blocks, so every K / V^T operand read from LDS feeds QB MFMAs.
+// SPLIT selects the three-MFMA score path.
+template <typename T, int HD, int QB, bool SPLIT, typename SM>
 __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int h, int q0, int row_cap,
                                           int L) {
   using TL = Tile<T, HD>;
+  constexpr int WROWS = 32 * QB;
+  constexpr int TROWS = 4 * WROWS;
   const int tid = threadIdx.x;
   const int w = tid / kWave;
   const int lane = tid % kWave;
   const int hl = lane / 32;
   const int ln = lane % 32;
-  const int qw0 = q0 + 32 * w;
-  const int qi = qw0 + ln;
+  const int qw0 = q0 + WROWS * w;
 
-  const int kv_end = a.causal ? min(q0 + BM, L) : L;
+  const int kv_end = a.causal ? min(q0 + TROWS, L) : L;
   const int n_kv = kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
   // Last key this wave needs (inclusive); waves whose rows are all padding
   // (or beyond row_cap) compute nothing.
-  int wave_last_key = a.causal ? min(qw0 + 31, kv_end - 1) : kv_end - 1;
+  int wave_last_key = a.causal ? min(qw0 + WROWS - 1, kv_end - 1) : kv_end - 1;
   if (qw0 >= L || qw0 >= row_cap) wave_last_key = -1;
 
-  // Q^T as the B operand: lane holds query qi, dims 16*ks + 8*hl .. +7.
-  half8_t qf[TL::KS];
-  half8_t qlo[SPLIT ? TL::KS : 1];
+  // Q^T as the B operand: lane holds query qw0 + 32*qb + ln, dims 16*ks + 8*hl .. +7.
+  half8_t qf[QB][TL::KS];
+  half8_t qlo[QB][SPLIT ? TL::KS : 1];
   {
     const T* qp = reinterpret_cast<const T*>(a.q);
-    const bool in = qi < a.S;
-    const int64_t base = a.vq.row(b, h, in ? qi : 0);
 #pragma unroll
-    for (int ks = 0; ks < TL::KS; ++ks) {
-      const int d0 = 16 * ks + 8 * hl;
+    for (int qb = 0; qb < QB; ++qb) {
+      const int qi = qw0 + 32 * qb + ln;
+      const bool in = qi < a.S;
+      const int64_t base = a.vq.row(b, h, in ? qi : 0);
 #pragma unroll
-      for (int e = 0; e < 8; e += Vec16<T>::N) {
-        Vec16<T> x;
-        if (in) x.load(qp + base + d0 + e); else x.zero();
+      for (int ks = 0; ks < TL::KS; ++ks) {
+        const int d0 = 16 * ks + 8 * hl;
 #pragma unroll
-        for (int j = 0; j < Vec16<T>::N; ++j) {
-          const float y = x.get(j) * a.qscale;
-          const half_t hi = (half_t)y;
-          qf[ks][e + j] = hi;
-          if constexpr (SPLIT) qlo[ks][e + j] = (half_t)(y - (float)hi);
+        for (int e = 0; e < 8; e += Vec16<T>::N) {
+          Vec16<T> x;
+          if (in) x.load(qp + base + d0 + e); else x.zero();
+#pragma unroll
+          for (int j = 0; j < Vec16<T>::N; ++j) {
+            const float y = x.get(j) * a.qscale;
+            const half_t hi = (half_t)y;
+            qf[qb][ks][e + j] = hi;
+            if constexpr (SPLIT) qlo[qb][ks][e + j] = (half_t)(y - (float)hi);
+          }
         }
       }
     }
   }
 
-  float16_t oacc[TL::DB];
+  float16_t oacc[QB][TL::DB];
+  float m_run[QB], l_run[QB];
 #pragma unroll
-  for (int db = 0; db < TL::DB; ++db)
+  for (int qb = 0; qb < QB; ++qb) {
+    m_run[qb] = -__builtin_inff();
+    l_run[qb] = 0.f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) oacc[db][r] = 0.f;
-  float m_run = -__builtin_inff();
-  float l_run = 0.f;
+    for (int db = 0; db < TL::DB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oacc[qb][db][r] = 0.f;
+  }
 
   KVStage<T, HD> stage;
   if (n_kv > 0) {
@@ -219,71 +230,98 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
     if (kt + 1 < n_kv) stage.load(a, b, h, kv0 + BN, tid);
 
     if (kv0 <= wave_last_key) {
-      float16_t sacc[2];
+      // Scores come out of the MFMA already shifted by the running max: the
+      // accumulator starts at -m_run (0 on the first tile, where m_run is set).
+      const bool first = kv0 == 0;
+      float16_t sacc[QB][2];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
+      for (int qb = 0; qb < QB; ++qb) {
+        const float c_init = first ? 0.f : -m_run[qb];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) sacc[qb][kb][r] = c_init;
+      }
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int ks = 0; ks < TL::KS; ++ks) {
           const half8_t kf = *reinterpret_cast<const half8_t*>(&sm.k[cur][kb * 32 + ln][16 * ks + 8 * hl]);
           if constexpr (SPLIT) {
             const half8_t kl = *reinterpret_cast<const half8_t*>(&sm.klo[cur][kb * 32 + ln][16 * ks + 8 * hl]);
-            sacc[kb] = mfma32(kl, qf[ks], sacc[kb]);
-            sacc[kb] = mfma32(kf, qlo[ks], sacc[kb]);
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) {
+              sacc[qb][kb] = mfma32(kl, qf[qb][ks], sacc[qb][kb]);
+              sacc[qb][kb] = mfma32(kf, qlo[qb][ks], sacc[qb][kb]);
+            }
           }
-          sacc[kb] = mfma32(kf, qf[ks], sacc[kb]);
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) sacc[qb][kb] = mfma32(kf, qf[qb][ks], sacc[qb][kb]);
         }
-      }
-      // Mask keys past the diagonal (causal) or past the valid length.
-      const bool need_mask = a.causal ? (kv0 + BN - 1 > qw0) : (kv0 + BN > L);
-      if (need_mask) {
-        const int lim = a.causal ? qi : L - 1;
+
+      half8_t pf[QB][4];
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        const int qb0 = qw0 + 32 * qb;
+        const int qi = qb0 + ln;
+        // Mask keys past the diagonal (causal) or past the valid length.
+        const bool need_mask = a.causal ? (kv0 + BN - 1 > qb0) : (kv0 + BN > L);
+        if (need_mask) {
+          const int lim = a.causal ? qi : L - 1;
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int key = kv0 + kb * 32 + 8 * (r / 4) + 4 * hl + (r % 4);
+              if (key > lim) sacc[qb][kb][r] = -__builtin_inff();
+            }
+        }
+        float t_max = sacc[qb][0][0];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = kv0 + kb * 32 + 8 * (r / 4) + 4 * hl + (r % 4);
-            if (key > lim) sacc[kb][r] = -__builtin_inff();
-          }
-      }
-      float mt_loc = sacc[0][0];
+          for (int r = 0; r < 16; ++r) t_max = fmaxf(t_max, sacc[qb][kb][r]);
+        t_max = pair_max(t_max);
+        // Lazy rescaling: the reference point moves only when a row's max grows
+        // by more than 2^8 (p <= 256 is exact enough in fp16 and harmless in the
+        // fp32 accumulators); the first tile always sets it.
+        const float shift = first ? t_max : (t_max > kRescaleLog2 ? t_max : 0.f);
+        if (first || __any(shift != 0.f)) {
+          const float alpha = first ? 0.f : fast_exp2(-shift);
+          m_run[qb] = first ? shift : m_run[qb] + shift;
+          l_run[qb] *= alpha;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+          for (int db = 0; db < TL::DB; ++db)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mt_loc = fmaxf(mt_loc, sacc[kb][r]);
-      mt_loc = fmaxf(mt_loc, xor32(mt_loc));
-      const float m_new = fmaxf(m_run, mt_loc);
-      const float alpha = fast_exp2(m_run - m_new);
-      m_run = m_new;
-      float psum = 0.f;
+            for (int r = 0; r < 16; ++r) oacc[qb][db][r] *= alpha;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+          for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p = fast_exp2(sacc[kb][r] - m_new);
-          sacc[kb][r] = p;
-          psum += p;
+            for (int r = 0; r < 16; ++r) sacc[qb][kb][r] -= shift;
         }
-      l_run = l_run * alpha + psum;
+        // P = exp2(S) rounded to fp16; the row sum adds the same rounded values.
 #pragma unroll
-      for (int db = 0; db < TL::DB; ++db)
+        for (int s = 0; s < 4; ++s)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+          for (int j = 0; j < 8; ++j) pf[qb][s][j] = (half_t)fast_exp2(sacc[qb][s / 2][8 * (s % 2) + j]);
+        float psum = 0.f;
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+          for (int j = 0; j < 8; j += 2)
+            psum = __builtin_amdgcn_fdot2(half2_t{pf[qb][s][j], pf[qb][s][j + 1]},
+                                          half2_t{(half_t)1.f, (half_t)1.f}, psum, false);
+        l_run[qb] += psum;
+      }
       // O^T += V^T P^T over four 16-key steps.
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int kb = s / 2;
-        const int r0 = 8 * (s % 2);
-        half8_t pf;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) pf[j] = (half_t)sacc[kb][r0 + j];
+      for (int s = 0; s < 4; ++s)
 #pragma unroll
         for (int db = 0; db < TL::DB; ++db) {
           const half8_t vf = *reinterpret_cast<const half8_t*>(&sm.vt[cur][db * 32 + ln][16 * s + 8 * hl]);
-          oacc[db] = mfma32(vf, pf, oacc[db]);
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) oacc[qb][db] = mfma32(vf, pf[qb][s], oacc[qb][db]);
         }
-      }
     }
 
     if (kt + 1 < n_kv) stage.template store<SPLIT>(sm, cur ^ 1, tid);
@@ -291,29 +329,32 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
   }
 
   // Epilogue: combine the two half-row sums, normalise, store.
-  const float l_tot = l_run + xor32(l_run);
-  if (qi < row_cap) {
-    const float inv = (qi < L && l_tot > 0.f) ? 1.f / l_tot : 0.f;
-    T* op = reinterpret_cast<T*>(a.o) + a.vo.row(b, h, qi);
 #pragma unroll
-    for (int db = 0; db < TL::DB; ++db)
+  for (int qb = 0; qb < QB; ++qb) {
+    const int qi = qw0 + 32 * qb + ln;
+    const float l_tot = pair_sum(l_run[qb]);
+    if (qi < row_cap) {
+      const float inv = (qi < L && l_tot > 0.f) ? 1.f / l_tot : 0.f;
+      T* op = reinterpret_cast<T*>(a.o) + a.vo.row(b, h, qi);
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d0 = db * 32 + 8 * g + 4 * hl;
-        if constexpr (sizeof(T) == 4) {
-          float4_t v4 = {oacc[db][4 * g] * inv, oacc[db][4 * g + 1] * inv, oacc[db][4 * g + 2] * inv,
-                         oacc[db][4 * g + 3] * inv};
-          *reinterpret_cast<float4_t*>(op + d0) = v4;
-        } else {
-          half4_t v4 = {(half_t)(oacc[db][4 * g] * inv), (half_t)(oacc[db][4 * g + 1] * inv),
-                        (half_t)(oacc[db][4 * g + 2] * inv), (half_t)(oacc[db][4 * g + 3] * inv)};
-          *reinterpret_cast<half4_t*>(op + d0) = v4;
+      for (int db = 0; db < TL::DB; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d0 = db * 32 + 8 * g + 4 * hl;
+          if constexpr (sizeof(T) == 4) {
+            *reinterpret_cast<float4_t*>(op + d0) = float4_t{oacc[qb][db][4 * g] * inv, oacc[qb][db][4 * g + 1] * inv,
+                                                              oacc[qb][db][4 * g + 2] * inv, oacc[qb][db][4 * g + 3] * inv};
+          } else {
+            *reinterpret_cast<half4_t*>(op + d0) =
+                half4_t{(half_t)(oacc[qb][db][4 * g] * inv), (half_t)(oacc[qb][db][4 * g + 1] * inv),
+                        (half_t)(oacc[qb][db][4 * g + 2] * inv), (half_t)(oacc[qb][db][4 * g + 3] * inv)};
+          }
         }
-      }
+    }
   }
 }
 
-template <typename T, int HD, bool SPLIT_OK>
+template <typename T, int HD, int QB, bool SPLIT_OK>
 __global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnArgs a) {
   __shared__ Smem<HD, SPLIT_OK> sm;
 
@@ -326,7 +367,7 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnArgs a) {
   const int mt = a.n_mtiles - 1 - logical % a.n_mtiles;
   const int b = bh / a.H;
   const int h = bh % a.H;
-  const int q0 = mt * BM;
+  const int q0 = mt * 128 * QB;
   int row_cap = a.S;
   if (a.row_limit != nullptr) row_cap = min(row_cap, max(0, a.row_limit[bh]));
   if (q0 >= row_cap) return;
@@ -335,21 +376,38 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnArgs a) {
 
   if constexpr (SPLIT_OK) {
     if (a.qk_split[bh] != 0) {
-      attn_tile<T, HD, true>(a, sm, b, h, q0, row_cap, L);
+      attn_tile<T, HD, QB, true>(a, sm, b, h, q0, row_cap, L);
       return;
     }
   }
-  attn_tile<T, HD, false>(a, sm, b, h, q0, row_cap, L);
+  attn_tile<T, HD, QB, false>(a, sm, b, h, q0, row_cap, L);
 }
 
+template <typename T, int HD, int QB>
+int launch_qb(AttnArgs a, hipStream_t stream) {
+  a.n_mtiles = (a.S + 128 * QB - 1) / (128 * QB);
+  a.total_tiles = a.B * a.H * a.n_mtiles;
+  a.per_xcd = (a.total_tiles + kNumXcd - 1) / kNumXcd;
+  const int grid = a.per_xcd * kNumXcd;
+  if constexpr (QB == 1) {
+    if (a.qk_split != nullptr) {
+      hipLaunchKernelGGL((attn_fwd_kernel<T, HD, QB, true>), dim3(grid), dim3(NT), 0, stream, a);
+      return tjh::launch_status();
+    }
+  }
+  hipLaunchKernelGGL((attn_fwd_kernel<T, HD, QB, false>), dim3(grid), dim3(NT), 0, stream, a);
+  return tjh::launch_status();
+}
+
+// Two query blocks per wave halve LDS operand traffic per MFMA. They fit the
+// register budget only for head_dim <= 64 without split scores, and need
+// sequences long enough to fill 256-row tiles.
 template <typename T, int HD>
 int launch(const AttnArgs& a, hipStream_t stream) {
-  const int grid = a.per_xcd * kNumXcd;
-  if (a.qk_split != nullptr)
-    hipLaunchKernelGGL((attn_fwd_kernel<T, HD, true>), dim3(grid), dim3(NT), 0, stream, a);
-  else
-    hipLaunchKernelGGL((attn_fwd_kernel<T, HD, false>), dim3(grid), dim3(NT), 0, stream, a);
-  return tjh::launch_status();
+  if constexpr (HD <= 64) {
+    if (a.S >= 512 && a.qk_split == nullptr) return launch_qb<T, HD, 2>(a, stream);
+  }
+  return launch_qb<T, HD, 1>(a, stream);
 }
 
 template <typename T>
@@ -373,7 +431,7 @@ extern "C" int tj_attn_fwd(const void* q, const void* k, const void* v, void* o,
                            const int32_t* row_limit, const int32_t* qk_split, hipStream_t stream) {
   if (dtype != TJ_F32 && dtype != TJ_F16) return TJ_ERR_DTYPE;
   if (B < 0 || H <= 0 || S < 0 || D <= 0) return TJ_ERR_SHAPE;
-  if (B * H * ((S + 127) / 128) >= (int64_t(1) << 31)) return TJ_ERR_SHAPE;
+  if (B * H * ((S + 127) / 128) >= (int64_t(1) << 31) || S >= (int64_t(1) << 30)) return TJ_ERR_SHAPE;
   if (D != 32 && D != 64 && D != 128) return TJ_ERR_UNSUPPORTED;
   if (B == 0 || S == 0) return TJ_OK;
   if (!q || !k || !v || !o) return TJ_ERR_SHAPE;
@@ -393,9 +451,6 @@ extern "C" int tj_attn_fwd(const void* q, const void* k, const void* v, void* o,
   a.valid_len = valid_len;
   a.row_limit = row_limit;
   a.qk_split = qk_split;
-  a.n_mtiles = (int)((S + tj::BM - 1) / tj::BM);
-  a.total_tiles = (int)(B * H) * a.n_mtiles;
-  a.per_xcd = (a.total_tiles + tj::kNumXcd - 1) / tj::kNumXcd;
   if (dtype == TJ_F32) return tj::dispatch_hd<float>(a, D, stream);
   return tj::dispatch_hd<half_t>(a, D, stream);
 }

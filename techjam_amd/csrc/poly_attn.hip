@@ -266,8 +266,8 @@ __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int 
   for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
     for (int j = 0; j < 8; ++j) den_l += (float)aB[ks][j] * zs[16 * ks + 8 * hl + j];
-  den_q += xor32(den_q);
-  den_l += xor32(den_l);
+  den_q = pair_sum(den_q);
+  den_l = pair_sum(den_l);
 
   // Exact diagonal block: keys [t0, min(t1, row0 + 128)), no max subtraction.
   float16_t accd[2];
@@ -321,7 +321,7 @@ __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int 
     if (kt + 1 < n_kt) tile.store_diag(kb[cur ^ 1], vt[cur ^ 1], tid);
     __syncthreads();
   }
-  den_d += xor32(den_d);
+  den_d = pair_sum(den_d);
 
   if (qi >= a.t1 || qi < a.prefix_end) return;
   const float c0 = a.coeffs[3 * m], c1 = a.coeffs[3 * m + 1], c2 = a.coeffs[3 * m + 2];

@@ -32,7 +32,27 @@ __device__ __forceinline__ float16_t mfma32(half8_t a, half8_t b, float16_t c) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-__device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32, kWave); }
+// Reductions over the lane pair (l, l ^ 32) through v_permlane32_swap, a VALU
+// op on gfx950, instead of an LDS permute. With both operands equal the swap
+// returns x[l] and x[l ^ 32] in its two results (which one lands where
+// depends on the half of the wave); max and sum do not care, and both lanes of
+// a pair get bitwise identical results.
+__device__ __forceinline__ void pair_values(float x, float& a, float& b) {
+  const unsigned u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float pair_max(float x) {
+  float a, b;
+  pair_values(x, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  float a, b;
+  pair_values(x, a, b);
+  return a + b;
+}
 
 // 16-byte vector of input elements: 4 floats or 8 halves, widened to fp32.
 template <typename T>
