@@ -78,6 +78,10 @@ const char* tj_error_string(int code);
  * dtype: TJ_F32 or TJ_F16 (q, k, v and o share it).
  * valid_len: device int32[B] or NULL. row_limit, qk_split: device
  * int32[B*H] or NULL.
+ * Strides are in elements with a unit innermost stride; row starts must be
+ * 16-byte aligned (TJ_ERR_ALIGN otherwise). The K and V rows of one (b,h) are
+ * read through 31-bit byte offsets: their sequence stride must be >= 0 and
+ * ((S-1)*stride + D) * element size < 2^31 (TJ_ERR_UNSUPPORTED otherwise).
  */
 int tj_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype,
                 int64_t B, int64_t H, int64_t S, int64_t D,

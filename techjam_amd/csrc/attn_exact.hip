@@ -23,6 +23,8 @@
 //     keys j <= i < L) and is not applied; padded rows i >= L are written as 0.
 //   * Grid: tile ids are remapped so that all query tiles of one (b, h) land on
 //     one XCD (K/V stay in that XCD's L2), heaviest (last) query tile first.
+//     Launches with row limits, whose work sits on a few (b, h), instead
+//     spread every (b, h) over all XCDs.
 //   * Heads flagged in qk_split compute QK^T from a two-term fp16 expansion of
 //     q and k (x = hi + lo, both fp16) with three MFMAs -- hi.hi + hi.lo +
 //     lo.hi -- which restores fp32-level score accuracy where the score range
@@ -36,6 +38,7 @@ constexpr int BN = 64;     // keys per tile
 constexpr int NT = 256;    // threads per workgroup
 constexpr int PAD = 8;     // fp16 padding per LDS row (16 bytes)
 constexpr float kRescaleLog2 = 8.f;  // lazy-rescale threshold of the running max (log2 units)
+constexpr int kBufferFlags = 0x00020000;  // raw (untyped) buffer resource word 3 on gfx950
 
 struct AttnArgs {
   const void* q;
@@ -52,6 +55,7 @@ struct AttnArgs {
   int n_mtiles;
   int total_tiles;
   int per_xcd;
+  int balanced;  // row_limit launches: spread every (b, h) over all XCDs
 };
 
 template <typename T, int HD>
@@ -83,36 +87,53 @@ struct Smem<HD, true> : SmemBase<HD> {
 // Global -> register staging of one key tile. Unit u covers keys 4g .. 4g+3 of
 // the tile and one 16-byte column vector c; lanes 4n .. 4n+3 share g so a
 // 16-lane LDS store phase touches 4 rows x 4 columns.
+//
+// K and V are read with bounds-checked buffer loads: one resource per (b, h)
+// spans rows 0 .. S-1 (byte offsets fit 31 bits, checked on the host), so
+// keys at or past S read as zeros without a branch, and the per-tile address
+// arithmetic is scalar: lane offset (4g, c) + scalar offset (kv0 + r) * stride.
 template <typename T, int HD>
 struct KVStage {
   using TL = Tile<T, HD>;
   Vec16<T> kx[TL::UPT][4];
   Vec16<T> vx[TL::UPT][4];
+  __amdgpu_buffer_rsrc_t rk, rv;
+  uint32_t koff[TL::UPT], voff[TL::UPT];
+  uint32_t kstep, vstep;  // bytes per key row
 
   __device__ __forceinline__ static void unit_coords(int u, int& g, int& c) {
     g = (u >> 2) & 15;
     c = (u & 3) | ((u >> 6) << 2);
   }
 
-  __device__ __forceinline__ void load(const AttnArgs& a, int b, int h, int kv0, int tid) {
-    const T* kp = reinterpret_cast<const T*>(a.k);
-    const T* vp = reinterpret_cast<const T*>(a.v);
+  __device__ __forceinline__ void init(const AttnArgs& a, int b, int h, int tid) {
+    const T* kp = reinterpret_cast<const T*>(a.k) + a.vk.row(b, h, 0);
+    const T* vp = reinterpret_cast<const T*>(a.v) + a.vv.row(b, h, 0);
+    kstep = (uint32_t)(a.vk.ss * (int64_t)sizeof(T));
+    vstep = (uint32_t)(a.vv.ss * (int64_t)sizeof(T));
+    const int kbytes = (int)((int64_t)(a.S - 1) * kstep + HD * (int64_t)sizeof(T));
+    const int vbytes = (int)((int64_t)(a.S - 1) * vstep + HD * (int64_t)sizeof(T));
+    rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(kp), (short)0, kbytes, kBufferFlags);
+    rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(vp), (short)0, vbytes, kBufferFlags);
 #pragma unroll
     for (int p = 0; p < TL::UPT; ++p) {
-      const int u = tid + p * NT;
-      if (u < TL::UNITS) {
-        int g, c;
-        unit_coords(u, g, c);
+      int g, c;
+      unit_coords(tid + p * NT, g, c);
+      koff[p] = 4 * g * kstep + c * TL::VEC * (uint32_t)sizeof(T);
+      voff[p] = 4 * g * vstep + c * TL::VEC * (uint32_t)sizeof(T);
+    }
+  }
+
+  __device__ __forceinline__ void load(int kv0, int tid) {
+#pragma unroll
+    for (int p = 0; p < TL::UPT; ++p) {
+      if (tid + p * NT < TL::UNITS) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int key = kv0 + 4 * g + r;
-          if (key < a.S) {
-            kx[p][r].load(kp + a.vk.row(b, h, key) + c * TL::VEC);
-            vx[p][r].load(vp + a.vv.row(b, h, key) + c * TL::VEC);
-          } else {
-            kx[p][r].zero();
-            vx[p][r].zero();
-          }
+          kx[p][r].v = __builtin_bit_cast(decltype(kx[p][r].v),
+                                          __builtin_amdgcn_raw_buffer_load_b128(rk, koff[p], (kv0 + r) * kstep, 0));
+          vx[p][r].v = __builtin_bit_cast(decltype(vx[p][r].v),
+                                          __builtin_amdgcn_raw_buffer_load_b128(rv, voff[p], (kv0 + r) * vstep, 0));
         }
       }
     }
@@ -218,8 +239,9 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
   }
 
   KVStage<T, HD> stage;
+  stage.init(a, b, h, tid);
   if (n_kv > 0) {
-    stage.load(a, b, h, 0, tid);
+    stage.load(0, tid);
     stage.template store<SPLIT>(sm, 0, tid);
   }
   __syncthreads();
@@ -227,7 +249,7 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
   for (int kt = 0; kt < n_kv; ++kt) {
     const int cur = kt & 1;
     const int kv0 = kt * BN;
-    if (kt + 1 < n_kv) stage.load(a, b, h, kv0 + BN, tid);
+    if (kt + 1 < n_kv) stage.load(kv0 + BN, tid);
 
     if (kv0 <= wave_last_key) {
       // Scores come out of the MFMA already shifted by the running max: the
@@ -361,10 +383,23 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnArgs a) {
   // XCD-aware tile order: ids x, x+8, x+16, ... run on XCD x and take
   // consecutive logical tiles, i.e. all query tiles of a few (b, h).
   const int id = blockIdx.x;
-  const int logical = (id % kNumXcd) * a.per_xcd + id / kNumXcd;
-  if (logical >= a.total_tiles) return;
-  const int bh = logical / a.n_mtiles;
-  const int mt = a.n_mtiles - 1 - logical % a.n_mtiles;
+  int bh, mt;
+  if (a.balanced) {
+    // Row limits concentrate the work on a few (b, h) (e.g. the exact
+    // fallback heads of the guarded polynomial route). Query tiles are then
+    // issued heaviest first across all (b, h), with the (b, h) index rotated
+    // per query tile so that consecutive ids -- which the hardware deals out
+    // round-robin over the XCDs -- spread each (b, h) over every XCD.
+    const int bhn = a.B * a.H;
+    const int mrev = id / bhn;
+    bh = (id % bhn + mrev) % bhn;
+    mt = a.n_mtiles - 1 - mrev;
+  } else {
+    const int logical = (id % kNumXcd) * a.per_xcd + id / kNumXcd;
+    if (logical >= a.total_tiles) return;
+    bh = logical / a.n_mtiles;
+    mt = a.n_mtiles - 1 - logical % a.n_mtiles;
+  }
   const int b = bh / a.H;
   const int h = bh % a.H;
   const int q0 = mt * 128 * QB;
@@ -388,7 +423,8 @@ int launch_qb(AttnArgs a, hipStream_t stream) {
   a.n_mtiles = (a.S + 128 * QB - 1) / (128 * QB);
   a.total_tiles = a.B * a.H * a.n_mtiles;
   a.per_xcd = (a.total_tiles + kNumXcd - 1) / kNumXcd;
-  const int grid = a.per_xcd * kNumXcd;
+  a.balanced = a.row_limit != nullptr;
+  const int grid = a.balanced ? a.total_tiles : a.per_xcd * kNumXcd;
   if constexpr (QB == 1) {
     if (a.qk_split != nullptr) {
       hipLaunchKernelGGL((attn_fwd_kernel<T, HD, QB, true>), dim3(grid), dim3(NT), 0, stream, a);
@@ -438,6 +474,11 @@ extern "C" int tj_attn_fwd(const void* q, const void* k, const void* v, void* o,
   if (!tjh::view_ok(q, q_strides, dtype) || !tjh::view_ok(k, k_strides, dtype) ||
       !tjh::view_ok(v, v_strides, dtype) || !tjh::view_ok(o, o_strides, dtype))
     return TJ_ERR_ALIGN;
+  // K and V rows of one (b, h) are addressed with 31-bit byte offsets.
+  for (const int64_t* st : {k_strides, v_strides}) {
+    if (st[2] < 0 || ((S - 1) * st[2] + D) * tjh::elem_size(dtype) >= (int64_t(1) << 31))
+      return TJ_ERR_UNSUPPORTED;
+  }
 
   tj::AttnArgs a;
   a.q = q; a.k = k; a.v = v; a.o = o;

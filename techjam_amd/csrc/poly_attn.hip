@@ -27,6 +27,8 @@
 // Apply reads state shadow [c & 1] (the state before chunk c) while the update
 // writes shadow [(c + 1) & 1], so both roles of a chunk run in the same launch.
 // Heads whose guard flag is 0 exit at once (the exact kernel covers them).
+#include <type_traits>
+
 #include "tj_common.h"
 
 namespace tj {
@@ -53,9 +55,12 @@ constexpr size_t kGramShadow = kLinShadow + 2 * PD * PD * 2;     // fp16 [2][64]
 constexpr size_t kZsShadow = kGramShadow + 2 * PD * PD * 2;      // fp32 [2][128]
 constexpr size_t kPerHead = (kZsShadow + 2 * 128 * 4 + 255) & ~size_t(255);
 
-// LDS: apply = quad staging / diagonal tiles (36864) + a tile (16896);
+// LDS: apply = quad-state ring (49152) or diagonal tiles (36864), + a tile (16896);
 //      updates = two transposed token tiles, double buffered (36864).
-constexpr int kStageBytes = 4 * 64 * LP * 2;
+constexpr int kRing = 3;                        // quad-state stages in flight
+constexpr int kRingStage = 2 * PD * PD * 2;     // one stage: rows of two i, [2][64 v][64 j] fp16
+constexpr int kStageBytes = kRing * kRingStage;
+static_assert(kStageBytes >= 4 * 64 * LP * 2, "diagonal / update tiles must fit the ring area");
 constexpr int kATileBytes = 128 * AP * 2;
 constexpr int kSmemBytes = kStageBytes + kATileBytes;
 
@@ -150,6 +155,15 @@ struct TokTile {
   }
 };
 
+// Workgroup barrier without the memory fences of __syncthreads(): callers wait
+// for their own LDS traffic explicitly (s_waitcnt) before it. The empty asm
+// statements keep the compiler from moving memory accesses across.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 __device__ __forceinline__ half8_t mul8(half8_t x, half_t s) {
   half8_t r;
 #pragma unroll
@@ -164,7 +178,6 @@ template <typename T>
 __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int m, int qt, char* smem) {
   const int row0 = a.t0 + 128 * qt;
   if (row0 >= a.t1 || row0 + 128 <= a.prefix_end) return;
-  auto sst = reinterpret_cast<half_t(*)[64][LP]>(smem);                 // [4][64][LP]
   auto kb = reinterpret_cast<half_t(*)[64][LP]>(smem);                  // diag: [2][64][LP]
   auto vt = reinterpret_cast<half_t(*)[64][LP]>(smem + 2 * 64 * LP * 2);  // diag: [2][64][LP]
   auto at = reinterpret_cast<half_t(*)[AP]>(smem + kStageBytes);       // [128][AP]
@@ -195,15 +208,38 @@ __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int 
   }
 
   const half_t* qshadow = reinterpret_cast<const half_t*>(ws + kQuadShadow) + size_t(a.cur) * PD * PD * PD;
-  // Stage the shadow rows of two i (2 x 64 x 64 fp16) into LDS buffer `buf`.
-  auto stage = [&](int pair, int buf) {
+  // The quad state streams through a ring of kRing LDS stages by direct
+  // global->LDS copies, two stages ahead of the MFMAs (no registers held).
+  // The stages are distinct members, addressed with compile-time stage
+  // indices, so the compiler can tell the copies into one stage from reads of
+  // another and does not wait for every copy in flight.
+  // Stage layout: [ii][v][64 j] rows of 128 bytes whose eight 16-byte pieces
+  // are XOR-swizzled by (v >> 1) & 7, so that 16 lanes reading one piece
+  // column of 16 consecutive rows touch 16 distinct bank groups.
+  // Copy instruction `it` of wave w fills 1 KiB slot (4 it + w) of the stage;
+  // lane l fills 16-byte piece slot 64 (4 it + w) + l.
+  struct Ring {
+    char s0[kRingStage];
+    char s1[kRingStage];
+    char s2[kRingStage];
+  };
+  static_assert(kRing == 3, "the ring below has three members");
+  Ring& ring = *reinterpret_cast<Ring*>(smem);
+  auto stage_ptr = [&](auto st) -> char* {
+    if constexpr (decltype(st)::value == 0) return ring.s0;
+    else if constexpr (decltype(st)::value == 1) return ring.s1;
+    else return ring.s2;
+  };
+  auto issue = [&](int pair, auto st) {
+    char* base = stage_ptr(st);
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
-      const int e = tid + it * PT;          // 1024 16-byte pieces
-      const int ii = e >> 9, rem = e & 511;
-      const int vrow = rem >> 3, piece = rem & 7;
-      const half8_t x = *reinterpret_cast<const half8_t*>(qshadow + (size_t(2 * pair + ii) * PD + vrow) * PD + 8 * piece);
-      *reinterpret_cast<half8_t*>(&sst[2 * buf + ii][vrow][8 * piece]) = x;
+      const int slot = (4 * it + w) * 64 + lane;
+      const int ii = slot >> 9, vrow = (slot >> 3) & 63, pos = slot & 7;
+      const int piece = pos ^ ((vrow >> 1) & 7);
+      const half_t* src = qshadow + (size_t(2 * pair + ii) * PD + vrow) * PD + 8 * piece;
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                       (__attribute__((address_space(3))) void*)(base + (4 * it + w) * 1024), 16, 0, 0);
     }
   };
 
@@ -213,11 +249,12 @@ __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int 
 #pragma unroll
     for (int r = 0; r < 16; ++r) accq[vb][r] = 0.f;
 
-  stage(0, 0);
-  __syncthreads();
-  for (int p = 0; p < PD / 2; ++p) {
-    const int buf = p & 1;
-    if (p + 1 < PD / 2) stage(p + 1, buf ^ 1);
+  constexpr int kPairs = PD / 2;
+  // One ring step: MFMAs on pair p from stage st, after issuing pair p + 2.
+  auto step = [&](int p, auto st) {
+    constexpr int sv = decltype(st)::value;
+    if (p + 2 < kPairs) issue(p + 2, std::integral_constant<int, (sv + 2) % kRing>{});
+    const char* base = stage_ptr(st);
 #pragma unroll
     for (int ii = 0; ii < 2; ++ii) {
       const half_t ai = at[qrow][2 * p + ii];
@@ -226,13 +263,32 @@ __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int 
         const half8_t bop = mul8(aB[ks], ai);
 #pragma unroll
         for (int vb = 0; vb < 2; ++vb) {
-          const half8_t sa = *reinterpret_cast<const half8_t*>(&sst[2 * buf + ii][32 * vb + ln][16 * ks + 8 * hl]);
+          const int row = 32 * vb + ln, piece = 2 * ks + hl;
+          const half8_t sa = *reinterpret_cast<const half8_t*>(base + ii * (kRingStage / 2) + row * 128 +
+                                                               16 * (piece ^ ((row >> 1) & 7)));
           accq[vb] = mfma32(sa, bop, accq[vb]);
         }
       }
     }
-    __syncthreads();
+    // Pair p + 1 (this wave's copies) must have landed before the barrier;
+    // pair p + 2 may stay in flight. A plain barrier: __syncthreads() would
+    // also wait for every copy in flight.
+    if (p + 2 < kPairs) __builtin_amdgcn_s_waitcnt(0x0074);  // vmcnt(4) lgkmcnt(0)
+    else __builtin_amdgcn_s_waitcnt(0x0070);                 // vmcnt(0) lgkmcnt(0)
+    lds_barrier();
+  };
+  issue(0, std::integral_constant<int, 0>{});
+  issue(1, std::integral_constant<int, 1>{});
+  __builtin_amdgcn_s_waitcnt(0x0074);  // pair 0 landed; a tile stores done
+  lds_barrier();
+  for (int p = 0; p + 3 <= kPairs; p += 3) {
+    step(p, std::integral_constant<int, 0>{});
+    step(p + 1, std::integral_constant<int, 1>{});
+    step(p + 2, std::integral_constant<int, 2>{});
   }
+  static_assert(kPairs % 3 == 2, "tail below handles two pairs");
+  step(kPairs - 2, std::integral_constant<int, 0>{});
+  step(kPairs - 1, std::integral_constant<int, 1>{});
 
   // Linear numerator term S_lin^T a^T and the quadratic denominator G a^T
   // (operands straight from the L2-resident shadows).

@@ -79,7 +79,29 @@ def guarded_attention(
     if not enabled:
         scaled_dot_product_attention(q, k, v, is_causal=True, scale=scale, qk_split=g.split, out=out)
         return out, g
+    # The exact launch (prefix rows of the polynomial heads, every row of the
+    # fallback heads) writes rows disjoint from the polynomial kernel's, so it
+    # runs on a side stream, overlapping the chunk launches, which leave most
+    # of the GPU idle.
+    main = torch.cuda.current_stream(q.device)
+    side = _side_stream(q.device)
+    side.wait_stream(main)
+    with torch.cuda.stream(side):
+        scaled_dot_product_attention(q, k, v, is_causal=True, scale=scale, row_limit=g.row_limit,
+                                     qk_split=g.split, out=out)
+    for t in (q, k, v, out, g.row_limit, g.split):
+        t.record_stream(side)
     poly_rows(q, k, v, scale, g.coeffs, flags=g.flags, chunk=CHUNK, exact_prefix=_prefix(q.shape[2]), out=out)
-    scaled_dot_product_attention(q, k, v, is_causal=True, scale=scale, row_limit=g.row_limit,
-                                 qk_split=g.split, out=out)
+    main.wait_stream(side)
     return out, g
+
+
+_SIDE_STREAMS: dict = {}
+
+
+def _side_stream(device: torch.device) -> torch.cuda.Stream:
+    """One default-priority side stream per device, created on first use."""
+    key = torch.device(device).index
+    if key not in _SIDE_STREAMS:
+        _SIDE_STREAMS[key] = torch.cuda.Stream(device=device)
+    return _SIDE_STREAMS[key]

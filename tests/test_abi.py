@@ -79,6 +79,13 @@ def test_attn_rejects_bad_arguments_before_launching():
     assert L.tj_attn_fwd(*args, _lib.TJ_F32, 1, 4, 128, 64, st, odd, st, st, 0.125, 1, None, None, None, None) == _lib.TJ_ERR_ALIGN
     # empty problems are a successful no-op
     assert L.tj_attn_fwd(*args, _lib.TJ_F32, 0, 4, 128, 64, st, st, st, st, 0.125, 1, None, None, None, None) == _lib.TJ_OK
+    # K/V rows of one (b, h) must span less than 2 GiB (31-bit buffer offsets)...
+    huge = _strides(64 * 128 * 4, 64, 1 << 23, 1)
+    assert L.tj_attn_fwd(*args, _lib.TJ_F32, 1, 4, 128, 64, st, huge, st, st, 0.125, 1, None, None, None, None) == _lib.TJ_ERR_UNSUPPORTED
+    assert L.tj_attn_fwd(*args, _lib.TJ_F32, 1, 4, 128, 64, st, st, huge, st, 0.125, 1, None, None, None, None) == _lib.TJ_ERR_UNSUPPORTED
+    # ... and run forward in memory
+    back = _strides(64 * 128 * 4, 64, -64 * 4, 1)
+    assert L.tj_attn_fwd(*args, _lib.TJ_F32, 1, 4, 128, 64, st, back, st, st, 0.125, 1, None, None, None, None) == _lib.TJ_ERR_UNSUPPORTED
 
 
 def test_guard_rejects_bad_arguments_before_launching():
