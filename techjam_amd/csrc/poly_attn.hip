@@ -11,21 +11,25 @@
 //   S_quad[(i,j), v] += sum_t b_ti b_tj v_tv,  S_lin[j, v] += sum_t b_tj v_tv,
 //   G[i, j] += sum_t b_ti b_tj,  z[j] += sum_t b_tj,  S_const[v] += sum_t v_tv.
 //
-// One launch per chunk; every head owns 13 workgroups with three roles:
-//   * apply (4 per head, 128 rows each): quadratic term as
+// Launches advance four chunks at a time; in launch L every head owns 25
+// workgroups with three roles:
+//   * apply (4 per chunk, 128 rows each, for the four chunks whose start
+//     states the previous launch produced): quadratic term as
 //       y^T = sum_i S_i^T (a_i * a^T)  (S_i = rows (i, .) of S_quad),
 //     i.e. 64 MFMA GEMMs whose B operand is the fp16 product a_i*a_j built in
 //     registers -- phi2(a) never exists in memory; linear and denominator terms
 //     as three more small GEMMs; the exact diagonal block like the exact
 //     kernel (S^T = b a^T in registers, no max subtraction).
 //   * quad update (8 per head, 8 i-slices each): S_i += (b_i * b)^T v over the
-//     chunk's tokens, accumulated straight into MFMA accumulators that hold the
-//     fp32 master in its register image (the master's memory layout IS the
-//     accumulator layout, so loading and storing it is straight 16-byte copies).
-//     It also writes the fp16 shadow the next chunk's apply reads.
-//   * small-state update (1 per head): S_lin, G, z, S_const.
-// Apply reads state shadow [c & 1] (the state before chunk c) while the update
-// writes shadow [(c + 1) & 1], so both roles of a chunk run in the same launch.
+//     tokens of chunks [4L, 4L + 4), accumulated straight into MFMA
+//     accumulators that hold the fp32 master in its register image (the
+//     master's memory layout IS the accumulator layout, so loading and storing
+//     it is straight 16-byte copies, once per launch). After each chunk it
+//     writes the fp16 shadow of the state the apply of the next chunk reads.
+//   * small-state update (1 per head): S_lin, G, z, S_const, likewise.
+// State c (before chunk c) lives in shadow slot c % 8: a launch reads the
+// slots of states 4L-3 .. 4L and writes those of 4L+1 .. 4L+4, so applies and
+// updates of one launch never touch the same slot.
 // Heads whose guard flag is 0 exit at once (the exact kernel covers them).
 #include <type_traits>
 
@@ -37,9 +41,11 @@ namespace {
 constexpr int PD = 64;         // head dim (d = dv)
 constexpr int PC = 512;        // chunk length
 constexpr int PT = 256;        // threads per workgroup
-constexpr int NAPPLY = 4;      // apply workgroups per head (128 rows each)
+constexpr int NAPPLY = 4;      // apply workgroups per head and chunk (128 rows each)
 constexpr int NUPD = 8;        // quad-update workgroups per head (8 i-slices each)
-constexpr int NROLE = NAPPLY + NUPD + 1;
+constexpr int KG = 4;          // chunks per launch (update sub-chunks, apply groups)
+constexpr int NSLOT = 2 * KG;  // shadow slots: state_c lives in slot c % NSLOT
+constexpr int NROLE = KG * NAPPLY + NUPD + 1;
 constexpr int LP = 72;         // padded LDS row of 64 halves (144 bytes)
 constexpr int AP = 66;         // padded LDS row of the a tile (132 bytes, conflict-free u16 reads)
 
@@ -49,11 +55,11 @@ constexpr size_t kQuadImgBytes = size_t(PD) * 4 * 64 * 16 * 4;  // 1 MiB
 constexpr size_t kLinImg = kQuadImg + kQuadImgBytes;             // fp32 [2 jb][2 vb][64][16]
 constexpr size_t kGramImg = kLinImg + 4 * 64 * 16 * 4;           // fp32 [2 ib][2 jb][64][16]
 constexpr size_t kZsMaster = kGramImg + 4 * 64 * 16 * 4;         // fp32 z[64], S_const[64]
-constexpr size_t kQuadShadow = kZsMaster + 128 * 4;              // fp16 [2][64 i][64 v][64 j]
-constexpr size_t kLinShadow = kQuadShadow + 2 * size_t(PD) * PD * PD * 2;  // fp16 [2][64 v][64 j]
-constexpr size_t kGramShadow = kLinShadow + 2 * PD * PD * 2;     // fp16 [2][64][64] (symmetric)
-constexpr size_t kZsShadow = kGramShadow + 2 * PD * PD * 2;      // fp32 [2][128]
-constexpr size_t kPerHead = (kZsShadow + 2 * 128 * 4 + 255) & ~size_t(255);
+constexpr size_t kQuadShadow = kZsMaster + 128 * 4;              // fp16 [NSLOT][64 i][64 v][64 j]
+constexpr size_t kLinShadow = kQuadShadow + NSLOT * size_t(PD) * PD * PD * 2;  // fp16 [NSLOT][64 v][64 j]
+constexpr size_t kGramShadow = kLinShadow + NSLOT * PD * PD * 2;  // fp16 [NSLOT][64][64] (symmetric)
+constexpr size_t kZsShadow = kGramShadow + NSLOT * PD * PD * 2;   // fp32 [NSLOT][128]
+constexpr size_t kPerHead = (kZsShadow + NSLOT * 128 * 4 + 255) & ~size_t(255);
 
 // LDS: apply = quad-state ring (49152) or diagonal tiles (36864), + a tile (16896);
 //      updates = two transposed token tiles, double buffered (36864).
@@ -72,10 +78,9 @@ struct PolyArgs {
   View4 vq, vk, vv, vo;
   int H, S;
   float rs;             // sqrt(scale)
-  int t0, t1;           // chunk rows
+  int launch;           // launch index L: applies chunks (KG (L-1), KG L], updates [KG L, KG L + KG)
+  int n_chunks;
   int prefix_end;       // rows below are left to the exact kernel
-  int emit, update;     // roles active in this launch
-  int cur;              // shadow slot holding the state before this chunk
   const float* coeffs;  // [M][3]
   const int32_t* flags; // [M] or null
   char* ws;
@@ -175,9 +180,10 @@ __device__ __forceinline__ half8_t mul8(half8_t x, half_t s) {
 // Apply role: rows [row0, row0 + 128) of the chunk.
 // ---------------------------------------------------------------------------
 template <typename T>
-__device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int m, int qt, char* smem) {
-  const int row0 = a.t0 + 128 * qt;
-  if (row0 >= a.t1 || row0 + 128 <= a.prefix_end) return;
+__device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int m, int c, int qt, char* smem) {
+  const int t0 = c * PC, t1 = min(a.S, t0 + PC), slot = c % NSLOT;
+  const int row0 = t0 + 128 * qt;
+  if (row0 >= t1 || row0 + 128 <= a.prefix_end) return;
   auto kb = reinterpret_cast<half_t(*)[64][LP]>(smem);                  // diag: [2][64][LP]
   auto vt = reinterpret_cast<half_t(*)[64][LP]>(smem + 2 * 64 * LP * 2);  // diag: [2][64][LP]
   auto at = reinterpret_cast<half_t(*)[AP]>(smem + kStageBytes);       // [128][AP]
@@ -191,8 +197,8 @@ __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int 
   half8_t aB[4];
   {
     const T* qp = reinterpret_cast<const T*>(a.q);
-    const bool in = qi < a.t1;
-    const int64_t base = a.vq.row(b, h, in ? qi : a.t0);
+    const bool in = qi < t1;
+    const int64_t base = a.vq.row(b, h, in ? qi : t0);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       float x[8];
@@ -207,7 +213,7 @@ __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int 
     }
   }
 
-  const half_t* qshadow = reinterpret_cast<const half_t*>(ws + kQuadShadow) + size_t(a.cur) * PD * PD * PD;
+  const half_t* qshadow = reinterpret_cast<const half_t*>(ws + kQuadShadow) + size_t(slot) * PD * PD * PD;
   // The quad state streams through a ring of kRing LDS stages by direct
   // global->LDS copies, two stages ahead of the MFMAs (no registers held).
   // The stages are distinct members, addressed with compile-time stage
@@ -292,9 +298,9 @@ __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int 
 
   // Linear numerator term S_lin^T a^T and the quadratic denominator G a^T
   // (operands straight from the L2-resident shadows).
-  const half_t* lsh = reinterpret_cast<const half_t*>(ws + kLinShadow) + size_t(a.cur) * PD * PD;
-  const half_t* gsh = reinterpret_cast<const half_t*>(ws + kGramShadow) + size_t(a.cur) * PD * PD;
-  const float* zs = reinterpret_cast<const float*>(ws + kZsShadow) + a.cur * 128;
+  const half_t* lsh = reinterpret_cast<const half_t*>(ws + kLinShadow) + size_t(slot) * PD * PD;
+  const half_t* gsh = reinterpret_cast<const half_t*>(ws + kGramShadow) + size_t(slot) * PD * PD;
+  const float* zs = reinterpret_cast<const float*>(ws + kZsShadow) + slot * 128;
   float16_t accl[2], ug[2];
 #pragma unroll
   for (int blk = 0; blk < 2; ++blk)
@@ -332,16 +338,16 @@ __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int 
 #pragma unroll
     for (int r = 0; r < 16; ++r) accd[vb][r] = 0.f;
   float den_d = 0.f;
-  const int key_end = min(a.t1, row0 + 128);
-  const int n_kt = (key_end - a.t0 + 63) / 64;
+  const int key_end = min(t1, row0 + 128);
+  const int n_kt = (key_end - t0 + 63) / 64;
   const int wave_last = min(qw0 + 31, key_end - 1);
   TokTile<T> tile;
-  tile.load(a, b, h, a.t0, key_end, tid);
+  tile.load(a, b, h, t0, key_end, tid);
   tile.store_diag(kb[0], vt[0], tid);
   __syncthreads();
   for (int kt = 0; kt < n_kt; ++kt) {
     const int cur = kt & 1;
-    const int kv0 = a.t0 + 64 * kt;
+    const int kv0 = t0 + 64 * kt;
     if (kt + 1 < n_kt) tile.load(a, b, h, kv0 + 64, key_end, tid);
     if (kv0 <= wave_last) {
       float16_t s[2];
@@ -379,9 +385,9 @@ __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int 
   }
   den_d = pair_sum(den_d);
 
-  if (qi >= a.t1 || qi < a.prefix_end) return;
+  if (qi >= t1 || qi < a.prefix_end) return;
   const float c0 = a.coeffs[3 * m], c1 = a.coeffs[3 * m + 1], c2 = a.coeffs[3 * m + 2];
-  const float den = c0 * (float)a.t0 + c1 * den_l + c2 * den_q + den_d;
+  const float den = c0 * (float)t0 + c1 * den_l + c2 * den_q + den_d;
   const float inv = 1.f / den;
   T* op = reinterpret_cast<T*>(a.o) + a.vo.row(b, h, qi);
 #pragma unroll
@@ -409,18 +415,18 @@ __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int 
 // Streams the chunk's tokens through LDS as transposed fp16 tiles and calls
 // body(bt, vt, tok) for every 16-token MFMA k-step.
 template <typename T, typename Body>
-__device__ __forceinline__ void stream_tokens(const PolyArgs& a, int b, int h, char* smem, Body&& body) {
+__device__ __forceinline__ void stream_tokens(const PolyArgs& a, int b, int h, int t0, int t1, char* smem, Body&& body) {
   auto bt = reinterpret_cast<half_t(*)[64][LP]>(smem);
   auto vt = reinterpret_cast<half_t(*)[64][LP]>(smem + 2 * 64 * LP * 2);
   const int tid = threadIdx.x;
-  const int n_blk = (a.t1 - a.t0 + 63) / 64;
+  const int n_blk = (t1 - t0 + 63) / 64;
   TokTile<T> tile;
-  tile.load(a, b, h, a.t0, a.t1, tid);
+  tile.load(a, b, h, t0, t1, tid);
   tile.store_transposed(bt[0], vt[0], tid);
   __syncthreads();
   for (int blk = 0; blk < n_blk; ++blk) {
     const int cur = blk & 1;
-    if (blk + 1 < n_blk) tile.load(a, b, h, a.t0 + 64 * (blk + 1), a.t1, tid);
+    if (blk + 1 < n_blk) tile.load(a, b, h, t0 + 64 * (blk + 1), t1, tid);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) body(bt[cur], vt[cur], 16 * ks);
     if (blk + 1 < n_blk) tile.store_transposed(bt[cur ^ 1], vt[cur ^ 1], tid);
@@ -457,12 +463,23 @@ __device__ __forceinline__ void store_shadow_t(half_t* dst, const float16_t& acc
   }
 }
 
+// Chunks whose states this launch folds in: [c0, c1) (the final chunk's
+// update is never needed).
+__device__ __forceinline__ void update_range(const PolyArgs& a, int& c0, int& c1) {
+  c0 = KG * a.launch;
+  c1 = min(c0 + KG, a.n_chunks - 1);
+}
+
 template <typename T>
 __device__ void quad_update_role(const PolyArgs& a, char* ws, int b, int h, int ug, char* smem) {
+  int c0, c1;
+  update_range(a, c0, c1);
+  if (c0 >= c1) return;
   const int w = threadIdx.x / kWave, lane = threadIdx.x % kWave, hl = lane / 32, ln = lane % 32;
   const int i0 = 8 * ug + 2 * w;  // this wave's two i-slices
   float* img = reinterpret_cast<float*>(ws + kQuadImg);
-  // acc[ii][jb][vb] = D[j][v] block of S_i (rows j, columns v).
+  // acc[ii][jb][vb] = D[j][v] block of S_i (rows j, columns v). The fp32
+  // master stays in these registers across the launch's chunks.
   float16_t acc[2][2][2];
 #pragma unroll
   for (int ii = 0; ii < 2; ++ii)
@@ -471,42 +488,50 @@ __device__ void quad_update_role(const PolyArgs& a, char* ws, int b, int h, int 
 #pragma unroll
       for (int vb = 0; vb < 2; ++vb) load_img(img + ((size_t(i0 + ii) * 2 + jb) * 2 + vb) * 1024, acc[ii][jb][vb]);
 
-  stream_tokens<T>(a, b, h, smem, [&](half_t (*bt)[LP], half_t (*vt)[LP], int tk) {
-    const int t = tk + 8 * hl;
-    half8_t bj[2], vv[2];
+  for (int c = c0; c < c1; ++c) {
+    stream_tokens<T>(a, b, h, c * PC, min(a.S, c * PC + PC), smem, [&](half_t (*bt)[LP], half_t (*vt)[LP], int tk) {
+      const int t = tk + 8 * hl;
+      half8_t bj[2], vv[2];
 #pragma unroll
-    for (int x = 0; x < 2; ++x) {
-      bj[x] = *reinterpret_cast<const half8_t*>(&bt[32 * x + ln][t]);
-      vv[x] = *reinterpret_cast<const half8_t*>(&vt[32 * x + ln][t]);
-    }
-#pragma unroll
-    for (int ii = 0; ii < 2; ++ii) {
-      const half8_t bi = *reinterpret_cast<const half8_t*>(&bt[i0 + ii][t]);
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb) {
-        half8_t phi;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) phi[j] = bj[jb][j] * bi[j];
-#pragma unroll
-        for (int vb = 0; vb < 2; ++vb) acc[ii][jb][vb] = mfma32(phi, vv[vb], acc[ii][jb][vb]);
+      for (int x = 0; x < 2; ++x) {
+        bj[x] = *reinterpret_cast<const half8_t*>(&bt[32 * x + ln][t]);
+        vv[x] = *reinterpret_cast<const half8_t*>(&vt[32 * x + ln][t]);
       }
-    }
-  });
-
-  half_t* sh = reinterpret_cast<half_t*>(ws + kQuadShadow) + size_t(a.cur ^ 1) * PD * PD * PD;
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii) {
+        const half8_t bi = *reinterpret_cast<const half8_t*>(&bt[i0 + ii][t]);
+#pragma unroll
+        for (int jb = 0; jb < 2; ++jb) {
+          half8_t phi;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) phi[j] = bj[jb][j] * bi[j];
+#pragma unroll
+          for (int vb = 0; vb < 2; ++vb) acc[ii][jb][vb] = mfma32(phi, vv[vb], acc[ii][jb][vb]);
+        }
+      }
+    });
+    // fp16 shadow of state_{c+1} for the applies of the next launch.
+    half_t* sh = reinterpret_cast<half_t*>(ws + kQuadShadow) + size_t((c + 1) % NSLOT) * PD * PD * PD;
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+        for (int vb = 0; vb < 2; ++vb) store_shadow_t(sh + size_t(i0 + ii) * PD * PD, acc[ii][jb][vb], jb, vb);
+  }
 #pragma unroll
   for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
-      for (int vb = 0; vb < 2; ++vb) {
-        store_img(img + ((size_t(i0 + ii) * 2 + jb) * 2 + vb) * 1024, acc[ii][jb][vb]);
-        store_shadow_t(sh + size_t(i0 + ii) * PD * PD, acc[ii][jb][vb], jb, vb);
-      }
+      for (int vb = 0; vb < 2; ++vb) store_img(img + ((size_t(i0 + ii) * 2 + jb) * 2 + vb) * 1024, acc[ii][jb][vb]);
 }
 
 template <typename T>
 __device__ void small_update_role(const PolyArgs& a, char* ws, int b, int h, char* smem) {
+  int c0, c1;
+  update_range(a, c0, c1);
+  if (c0 >= c1) return;
   const int w = threadIdx.x / kWave, lane = threadIdx.x % kWave, hl = lane / 32, ln = lane % 32;
   float* lin_img = reinterpret_cast<float*>(ws + kLinImg);
   float* gram_img = reinterpret_cast<float*>(ws + kGramImg);
@@ -519,64 +544,80 @@ __device__ void small_update_role(const PolyArgs& a, char* ws, int b, int h, cha
 #pragma unroll
       for (int cb = 0; cb < 2; ++cb) load_img(img + (rb * 2 + cb) * 1024, acc[rb][cb]);
   }
-  float zsum = 0.f, csum = 0.f;
-  stream_tokens<T>(a, b, h, smem, [&](half_t (*bt)[LP], half_t (*vt)[LP], int tk) {
-    const int t = tk + 8 * hl;
-    if (w == 0) {  // S_lin[j][v] = sum_t b_tj v_tv
+  float z = 0.f, cs = 0.f;
+  if (w == 2) {
+    z = zs[lane];
+    cs = zs[64 + lane];
+  }
+  for (int c = c0; c < c1; ++c) {
+    float zsum = 0.f, csum = 0.f;
+    stream_tokens<T>(a, b, h, c * PC, min(a.S, c * PC + PC), smem, [&](half_t (*bt)[LP], half_t (*vt)[LP], int tk) {
+      const int t = tk + 8 * hl;
+      if (w == 0) {  // S_lin[j][v] = sum_t b_tj v_tv
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb) {
-        const half8_t bj = *reinterpret_cast<const half8_t*>(&bt[32 * jb + ln][t]);
+        for (int jb = 0; jb < 2; ++jb) {
+          const half8_t bj = *reinterpret_cast<const half8_t*>(&bt[32 * jb + ln][t]);
 #pragma unroll
-        for (int vb = 0; vb < 2; ++vb)
-          acc[jb][vb] = mfma32(bj, *reinterpret_cast<const half8_t*>(&vt[32 * vb + ln][t]), acc[jb][vb]);
+          for (int vb = 0; vb < 2; ++vb)
+            acc[jb][vb] = mfma32(bj, *reinterpret_cast<const half8_t*>(&vt[32 * vb + ln][t]), acc[jb][vb]);
+        }
+      } else if (w == 1) {  // G[i][j] = sum_t b_ti b_tj
+#pragma unroll
+        for (int ib = 0; ib < 2; ++ib) {
+          const half8_t bi = *reinterpret_cast<const half8_t*>(&bt[32 * ib + ln][t]);
+#pragma unroll
+          for (int jb = 0; jb < 2; ++jb)
+            acc[ib][jb] = mfma32(bi, *reinterpret_cast<const half8_t*>(&bt[32 * jb + ln][t]), acc[ib][jb]);
+        }
+      } else if (w == 2) {  // z[d] and S_const[d]: lane = dim, 16 tokens per step
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          zsum += (float)bt[lane][tk + j];
+          csum += (float)vt[lane][tk + j];
+        }
       }
-    } else if (w == 1) {  // G[i][j] = sum_t b_ti b_tj
+    });
+    const int nxt = (c + 1) % NSLOT;
+    if (w == 0) {
+      half_t* sh = reinterpret_cast<half_t*>(ws + kLinShadow) + size_t(nxt) * PD * PD;  // [v][j]
 #pragma unroll
-      for (int ib = 0; ib < 2; ++ib) {
-        const half8_t bi = *reinterpret_cast<const half8_t*>(&bt[32 * ib + ln][t]);
+      for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
-        for (int jb = 0; jb < 2; ++jb)
-          acc[ib][jb] = mfma32(bi, *reinterpret_cast<const half8_t*>(&bt[32 * jb + ln][t]), acc[ib][jb]);
-      }
-    } else if (w == 2) {  // z[d] and S_const[d]: lane = dim, 16 tokens per step
+        for (int vb = 0; vb < 2; ++vb) store_shadow_t(sh, acc[jb][vb], jb, vb);
+    } else if (w == 1) {
+      half_t* sh = reinterpret_cast<half_t*>(ws + kGramShadow) + size_t(nxt) * PD * PD;  // symmetric
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        zsum += (float)bt[lane][tk + j];
-        csum += (float)vt[lane][tk + j];
-      }
+      for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+        for (int jb = 0; jb < 2; ++jb) store_shadow_t(sh, acc[ib][jb], ib, jb);
+    } else if (w == 2) {
+      z += zsum;
+      cs += csum;
+      float* zsh = reinterpret_cast<float*>(ws + kZsShadow) + nxt * 128;
+      zsh[lane] = z;
+      zsh[64 + lane] = cs;
     }
-  });
-
-  const int nxt = a.cur ^ 1;
+  }
   if (w == 0) {
-    half_t* sh = reinterpret_cast<half_t*>(ws + kLinShadow) + size_t(nxt) * PD * PD;  // [v][j]
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
-      for (int vb = 0; vb < 2; ++vb) {
-        store_img(lin_img + (jb * 2 + vb) * 1024, acc[jb][vb]);
-        store_shadow_t(sh, acc[jb][vb], jb, vb);
-      }
+      for (int vb = 0; vb < 2; ++vb) store_img(lin_img + (jb * 2 + vb) * 1024, acc[jb][vb]);
   } else if (w == 1) {
-    half_t* sh = reinterpret_cast<half_t*>(ws + kGramShadow) + size_t(nxt) * PD * PD;  // symmetric
 #pragma unroll
     for (int ib = 0; ib < 2; ++ib)
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb) {
-        store_img(gram_img + (ib * 2 + jb) * 1024, acc[ib][jb]);
-        store_shadow_t(sh, acc[ib][jb], ib, jb);
-      }
+      for (int jb = 0; jb < 2; ++jb) store_img(gram_img + (ib * 2 + jb) * 1024, acc[ib][jb]);
   } else if (w == 2) {
-    const float z = zs[lane] + zsum;
-    const float c = zs[64 + lane] + csum;
     zs[lane] = z;
-    zs[64 + lane] = c;
-    float* zsh = reinterpret_cast<float*>(ws + kZsShadow) + nxt * 128;
-    zsh[lane] = z;
-    zsh[64 + lane] = c;
+    zs[64 + lane] = cs;
   }
 }
 
+// Roles of one head in launch L: KG * NAPPLY apply workgroups (chunk
+// KG (L-1) + 1 + j / NAPPLY, row block j % NAPPLY; launch 0 applies chunk 0
+// only), NUPD quad-update workgroups and one small-state update, the updates
+// folding in chunks [KG L, KG L + KG).
 template <typename T>
 __global__ __launch_bounds__(PT, 2) void poly_chunk_kernel(PolyArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kSmemBytes];
@@ -588,12 +629,14 @@ __global__ __launch_bounds__(PT, 2) void poly_chunk_kernel(PolyArgs a) {
   if (a.flags != nullptr && a.flags[m] == 0) return;
   const int b = m / a.H, h = m % a.H;
   char* ws = a.ws + size_t(m) * kPerHead;
-  if (role < NAPPLY) {
-    if (a.emit) apply_role<T>(a, ws, b, h, m, role, smem);
-  } else if (role < NAPPLY + NUPD) {
-    if (a.update) quad_update_role<T>(a, ws, b, h, role - NAPPLY, smem);
+  if (role < KG * NAPPLY) {
+    const int g = role / NAPPLY;
+    const int c = a.launch == 0 ? (g == 0 ? 0 : -1) : KG * (a.launch - 1) + 1 + g;
+    if (c >= 0 && c < a.n_chunks) apply_role<T>(a, ws, b, h, m, c, role % NAPPLY, smem);
+  } else if (role < KG * NAPPLY + NUPD) {
+    quad_update_role<T>(a, ws, b, h, role - KG * NAPPLY, smem);
   } else {
-    if (a.update) small_update_role<T>(a, ws, b, h, smem);
+    small_update_role<T>(a, ws, b, h, smem);
   }
 }
 
@@ -603,18 +646,18 @@ __global__ void zero_kernel(float4_t* p, size_t n) {
 }
 
 template <typename T>
-int run(PolyArgs a, int S, int chunk, size_t ws_bytes, hipStream_t stream) {
+int run(PolyArgs a, size_t ws_bytes, hipStream_t stream) {
   hipLaunchKernelGGL(zero_kernel, dim3(1024), dim3(256), 0, stream, reinterpret_cast<float4_t*>(a.ws),
                      ws_bytes / 16);
   if (hipGetLastError() != hipSuccess) return TJ_ERR_LAUNCH;
-  const int n_chunks = (S + chunk - 1) / chunk;
-  for (int c = 0; c < n_chunks; ++c) {
-    a.t0 = c * chunk;
-    a.t1 = min(S, a.t0 + chunk);
-    a.emit = a.t1 > a.prefix_end ? 1 : 0;
-    a.update = c + 1 < n_chunks ? 1 : 0;
-    a.cur = c & 1;
-    if (!a.emit && !a.update) continue;
+  // Launch L applies chunks (KG (L-1), KG L] and folds in chunks [KG L, KG L + KG).
+  const int n_launch = 1 + (a.n_chunks - 1 + KG - 1) / KG;
+  for (int L = 0; L < n_launch; ++L) {
+    const int last_applied = min(KG * L, a.n_chunks - 1);
+    const bool emits = min(a.S, (last_applied + 1) * PC) > a.prefix_end;
+    const bool updates = KG * L < a.n_chunks - 1;
+    if (!emits && !updates) continue;
+    a.launch = L;
     hipLaunchKernelGGL(poly_chunk_kernel<T>, dim3(a.per_xcd * kNumXcd), dim3(PT), 0, stream, a);
     if (hipGetLastError() != hipSuccess) return TJ_ERR_LAUNCH;
   }
@@ -664,6 +707,7 @@ extern "C" int tj_poly_attn_fwd(const void* q, const void* k, const void* v, voi
   a.ws = static_cast<char*>(workspace);
   a.total = (int)(B * H) * tj::NROLE;
   a.per_xcd = (a.total + tj::kNumXcd - 1) / tj::kNumXcd;
-  if (dtype == TJ_F32) return tj::run<float>(a, (int)S, (int)chunk, need, stream);
-  return tj::run<half_t>(a, (int)S, (int)chunk, need, stream);
+  a.n_chunks = (int)((S + tj::PC - 1) / tj::PC);
+  if (dtype == TJ_F32) return tj::run<float>(a, need, stream);
+  return tj::run<half_t>(a, need, stream);
 }
