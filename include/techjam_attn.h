@@ -146,6 +146,8 @@ size_t tj_poly_workspace_bytes(int64_t B, int64_t H, int64_t S, int64_t D, int64
  * or NULL; heads with flags[bh] == 0 are skipped entirely. Rows < exact_prefix
  * are not written: compute them with tj_attn_fwd (row_limit from the guard).
  * Only D == 64 and chunk == 512 are implemented.
+ * K and V rows of one (b,h) are read through 31-bit byte offsets, as in
+ * tj_attn_fwd (TJ_ERR_UNSUPPORTED otherwise).
  */
 int tj_poly_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype,
                      int64_t B, int64_t H, int64_t S, int64_t D,

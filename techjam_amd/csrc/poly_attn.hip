@@ -47,6 +47,7 @@ constexpr int KG = 4;          // chunks per launch (update sub-chunks, apply gr
 constexpr int NSLOT = 2 * KG;  // shadow slots: state_c lives in slot c % NSLOT
 constexpr int NROLE = KG * NAPPLY + NUPD + 1;
 constexpr int LP = 72;         // padded LDS row of 64 halves (144 bytes)
+constexpr int kBufferFlags = 0x00020000;  // raw (untyped) buffer resource word 3 on gfx950
 constexpr int AP = 66;         // padded LDS row of the a tile (132 bytes, conflict-free u16 reads)
 
 // Workspace of one head (byte offsets).
@@ -101,54 +102,70 @@ __device__ __forceinline__ void load_row4(const T* p, float out[4]) {
   }
 }
 
-// Global -> registers of one 64-token x 64-dim tile of k (scaled by rs) and v.
-// Unit = (4-token group g, 4-dim group c); one unit per thread.
+// Global -> registers of one 64-token x 64-dim tile of k and v. Unit =
+// (4-token group g, 4-dim group c); one unit per thread. Rows are read with
+// bounds-checked buffer loads (one resource per (b, h) spanning rows 0..S-1),
+// so tokens at or past S read as zeros without a branch, and nothing waits
+// on the loads before the tile is stored: k is scaled by rs at the store.
 template <typename T>
 struct TokTile {
   float kx[4][4];
   float vx[4][4];
+  __amdgpu_buffer_rsrc_t rk, rv;
+  uint32_t koff, voff, kstep, vstep;
   __device__ __forceinline__ static void coords(int tid, int& g, int& c) {
     g = (tid >> 2) & 15;
     c = (tid & 3) | ((tid >> 6) << 2);
   }
-  __device__ __forceinline__ void load(const PolyArgs& a, int b, int h, int tok0, int tok_end, int tid) {
+  __device__ __forceinline__ void init(const PolyArgs& a, int b, int h, int tid) {
     int g, c;
     coords(tid, g, c);
-    const T* kp = reinterpret_cast<const T*>(a.k);
-    const T* vp = reinterpret_cast<const T*>(a.v);
+    const T* kp = reinterpret_cast<const T*>(a.k) + a.vk.row(b, h, 0);
+    const T* vp = reinterpret_cast<const T*>(a.v) + a.vv.row(b, h, 0);
+    kstep = (uint32_t)(a.vk.ss * (int64_t)sizeof(T));
+    vstep = (uint32_t)(a.vv.ss * (int64_t)sizeof(T));
+    const int kbytes = (int)((int64_t)(a.S - 1) * kstep + PD * (int64_t)sizeof(T));
+    const int vbytes = (int)((int64_t)(a.S - 1) * vstep + PD * (int64_t)sizeof(T));
+    rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(kp), (short)0, kbytes, kBufferFlags);
+    rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(vp), (short)0, vbytes, kBufferFlags);
+    koff = 4 * g * kstep + 4 * c * (uint32_t)sizeof(T);
+    voff = 4 * g * vstep + 4 * c * (uint32_t)sizeof(T);
+  }
+  __device__ __forceinline__ void load(int tok0) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int t = tok0 + 4 * g + r;
-      if (t < tok_end) {
-        load_row4<T>(kp + a.vk.row(b, h, t) + 4 * c, kx[r]);
-        load_row4<T>(vp + a.vv.row(b, h, t) + 4 * c, vx[r]);
+      if constexpr (sizeof(T) == 4) {
+        const float4_t x = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, koff, (tok0 + r) * kstep, 0));
+        const float4_t y = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rv, voff, (tok0 + r) * vstep, 0));
 #pragma unroll
-        for (int e = 0; e < 4; ++e) kx[r][e] *= a.rs;
+        for (int e = 0; e < 4; ++e) { kx[r][e] = x[e]; vx[r][e] = y[e]; }
       } else {
+        const half4_t x = __builtin_bit_cast(half4_t, __builtin_amdgcn_raw_buffer_load_b64(rk, koff, (tok0 + r) * kstep, 0));
+        const half4_t y = __builtin_bit_cast(half4_t, __builtin_amdgcn_raw_buffer_load_b64(rv, voff, (tok0 + r) * vstep, 0));
 #pragma unroll
-        for (int e = 0; e < 4; ++e) kx[r][e] = vx[r][e] = 0.f;
+        for (int e = 0; e < 4; ++e) { kx[r][e] = (float)x[e]; vx[r][e] = (float)y[e]; }
       }
     }
   }
   // Both transposed ([dim][token], token order as given): the update roles.
-  __device__ __forceinline__ void store_transposed(half_t (*bt)[LP], half_t (*vt)[LP], int tid) const {
+  __device__ __forceinline__ void store_transposed(half_t (*bt)[LP], half_t (*vt)[LP], float rs, int tid) const {
     int g, c;
     coords(tid, g, c);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      half4_t hb = {(half_t)kx[0][e], (half_t)kx[1][e], (half_t)kx[2][e], (half_t)kx[3][e]};
+      half4_t hb = {(half_t)(kx[0][e] * rs), (half_t)(kx[1][e] * rs), (half_t)(kx[2][e] * rs), (half_t)(kx[3][e] * rs)};
       half4_t hv = {(half_t)vx[0][e], (half_t)vx[1][e], (half_t)vx[2][e], (half_t)vx[3][e]};
       *reinterpret_cast<half4_t*>(&bt[4 * c + e][4 * g]) = hb;
       *reinterpret_cast<half4_t*>(&vt[4 * c + e][4 * g]) = hv;
     }
   }
   // K row-major, V transposed in key_slot order: the diagonal block (as in the exact kernel).
-  __device__ __forceinline__ void store_diag(half_t (*kb)[LP], half_t (*vt)[LP], int tid) const {
+  __device__ __forceinline__ void store_diag(half_t (*kb)[LP], half_t (*vt)[LP], float rs, int tid) const {
     int g, c;
     coords(tid, g, c);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      half4_t hk = {(half_t)kx[r][0], (half_t)kx[r][1], (half_t)kx[r][2], (half_t)kx[r][3]};
+      half4_t hk = {(half_t)(kx[r][0] * rs), (half_t)(kx[r][1] * rs), (half_t)(kx[r][2] * rs), (half_t)(kx[r][3] * rs)};
       *reinterpret_cast<half4_t*>(&kb[4 * g + r][4 * c]) = hk;
     }
     const int slot = key_slot(4 * g);
@@ -342,13 +359,14 @@ __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int 
   const int n_kt = (key_end - t0 + 63) / 64;
   const int wave_last = min(qw0 + 31, key_end - 1);
   TokTile<T> tile;
-  tile.load(a, b, h, t0, key_end, tid);
-  tile.store_diag(kb[0], vt[0], tid);
+  tile.init(a, b, h, tid);
+  tile.load(t0);
+  tile.store_diag(kb[0], vt[0], a.rs, tid);
   __syncthreads();
   for (int kt = 0; kt < n_kt; ++kt) {
     const int cur = kt & 1;
     const int kv0 = t0 + 64 * kt;
-    if (kt + 1 < n_kt) tile.load(a, b, h, kv0 + 64, key_end, tid);
+    if (kt + 1 < n_kt) tile.load(kv0 + 64);
     if (kv0 <= wave_last) {
       float16_t s[2];
 #pragma unroll
@@ -380,7 +398,7 @@ __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int 
           accd[vb] = mfma32(vf, pf[st], accd[vb]);
         }
     }
-    if (kt + 1 < n_kt) tile.store_diag(kb[cur ^ 1], vt[cur ^ 1], tid);
+    if (kt + 1 < n_kt) tile.store_diag(kb[cur ^ 1], vt[cur ^ 1], a.rs, tid);
     __syncthreads();
   }
   den_d = pair_sum(den_d);
@@ -421,15 +439,16 @@ __device__ __forceinline__ void stream_tokens(const PolyArgs& a, int b, int h, i
   const int tid = threadIdx.x;
   const int n_blk = (t1 - t0 + 63) / 64;
   TokTile<T> tile;
-  tile.load(a, b, h, t0, t1, tid);
-  tile.store_transposed(bt[0], vt[0], tid);
+  tile.init(a, b, h, tid);
+  tile.load(t0);
+  tile.store_transposed(bt[0], vt[0], a.rs, tid);
   __syncthreads();
   for (int blk = 0; blk < n_blk; ++blk) {
     const int cur = blk & 1;
-    if (blk + 1 < n_blk) tile.load(a, b, h, t0 + 64 * (blk + 1), t1, tid);
+    if (blk + 1 < n_blk) tile.load(t0 + 64 * (blk + 1));
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) body(bt[cur], vt[cur], 16 * ks);
-    if (blk + 1 < n_blk) tile.store_transposed(bt[cur ^ 1], vt[cur ^ 1], tid);
+    if (blk + 1 < n_blk) tile.store_transposed(bt[cur ^ 1], vt[cur ^ 1], a.rs, tid);
     __syncthreads();
   }
 }
@@ -690,6 +709,11 @@ extern "C" int tj_poly_attn_fwd(const void* q, const void* k, const void* v, voi
   if (!tjh::view_ok(q, q_strides, dtype) || !tjh::view_ok(k, k_strides, dtype) ||
       !tjh::view_ok(v, v_strides, dtype) || !tjh::view_ok(o, o_strides, dtype))
     return TJ_ERR_ALIGN;
+  // K and V rows of one (b, h) are addressed with 31-bit byte offsets.
+  for (const int64_t* st : {k_strides, v_strides}) {
+    if (st[2] < 0 || ((S - 1) * st[2] + D) * tjh::elem_size(dtype) >= (int64_t(1) << 31))
+      return TJ_ERR_UNSUPPORTED;
+  }
   const size_t need = size_t(B * H) * tj::kPerHead;
   if (workspace == nullptr || workspace_bytes < need || !tjh::aligned16(workspace)) return TJ_ERR_WORKSPACE;
 
