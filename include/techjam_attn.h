@@ -157,6 +157,45 @@ int tj_poly_attn_fwd(const void* q, const void* k, const void* v, void* o, int d
                      const float* coeffs, const int32_t* flags,
                      void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/*
+ * Stand-alone polynomial kernels with the reference's tensor contract
+ * (src/kernels/poly_attention_triton.py:420-591: quad_apply, quad_update,
+ * causal_diag). The fused tj_poly_attn_fwd does not use them; they serve
+ * callers of the reference's kernel-level API. Shapes are [M, rows, cols]
+ * with a unit innermost stride and 16-byte aligned rows; strides are in
+ * elements. Only D == V == 64 is implemented (TJ_ERR_UNSUPPORTED otherwise;
+ * the Python wrappers zero-pad narrower heads).
+ *
+ * tj_quad_apply (quad_apply, :420-466): y[m,c,:] = sum_{i,j} a[m,c,i]
+ * a[m,c,j] s[m, i*D + j, :] with a, y fp16 and s fp32 or fp16 (s_dtype); s is
+ * rounded to fp16 before the products, so a master and its fp16 shadow give
+ * bitwise-identical y.
+ */
+int tj_quad_apply(const void* a, const void* s, void* y, int s_dtype, int64_t M, int64_t C, int64_t D,
+                  int64_t V, const int64_t a_strides[3], const int64_t s_strides[3],
+                  const int64_t y_strides[3], hipStream_t stream);
+
+/*
+ * tj_quad_update (quad_update, :469-530): s[m, i*D + j, :] +=
+ * sum_t b[m,t,i] b[m,t,j] v[m,t,:] in place, s fp32 (the running master),
+ * b, v fp16. When shadow is non-NULL (fp16, shaped like s) it receives the
+ * updated master rounded to fp16.
+ */
+int tj_quad_update(const void* b, const void* v, float* s, void* shadow, int64_t M, int64_t C, int64_t D,
+                   int64_t V, const int64_t b_strides[3], const int64_t v_strides[3],
+                   const int64_t s_strides[3], const int64_t shadow_strides[3], hipStream_t stream);
+
+/*
+ * tj_causal_diag (causal_diag, :533-591): w = tril(exp(a b^T)) with no max
+ * subtraction; num[m,c,:] = (w v)[c] (fp32), den[m*den_stride_m + c] =
+ * sum_j w[c,j] (fp32, of the fp16-rounded weights the product uses).
+ * a, b, v fp16.
+ */
+int tj_causal_diag(const void* a, const void* b, const void* v, float* num, float* den, int64_t M,
+                   int64_t C, int64_t D, int64_t V, const int64_t a_strides[3],
+                   const int64_t b_strides[3], const int64_t v_strides[3],
+                   const int64_t num_strides[3], int64_t den_stride_m, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

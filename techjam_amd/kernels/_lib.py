@@ -52,6 +52,18 @@ SIGNATURES = {
         [_vp, _vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _i64p, _i64p, _i64p, _i64p,
          _f32, _i64, _i64, _vp, _vp, _vp, ctypes.c_size_t, _vp],
     ),
+    "tj_quad_apply": (
+        _int,
+        [_vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _i64p, _i64p, _i64p, _vp],
+    ),
+    "tj_quad_update": (
+        _int,
+        [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64p, _i64p, _i64p, _i64p, _vp],
+    ),
+    "tj_causal_diag": (
+        _int,
+        [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64p, _i64p, _i64p, _i64p, _i64, _vp],
+    ),
 }
 
 _lock = threading.Lock()

@@ -126,3 +126,43 @@ def test_cpu_tensors_are_refused_not_computed():
     q = torch.randn(1, 2, 16, 64)
     with pytest.raises(UnsupportedCaseError):
         scaled_dot_product_attention(q, q, q, is_causal=True)
+
+
+def _s3(*s):
+    return (ctypes.c_int64 * 3)(*s)
+
+
+def test_poly_parts_reject_bad_arguments_before_launching():
+    from techjam_amd.kernels import _lib
+
+    L = _lib.lib()
+    st = _s3(128 * 64, 64, 1)
+    ss = _s3(4096 * 64, 64, 1)
+    # the kernels are written for D = V = 64
+    assert L.tj_quad_apply(16, 16, 16, _lib.TJ_F32, 2, 128, 32, 64, st, ss, st, None) == _lib.TJ_ERR_UNSUPPORTED
+    assert L.tj_quad_apply(16, 16, 16, 9, 2, 128, 64, 64, st, ss, st, None) == _lib.TJ_ERR_DTYPE
+    assert L.tj_quad_apply(16, 16, 16, _lib.TJ_F32, -1, 128, 64, 64, st, ss, st, None) == _lib.TJ_ERR_SHAPE
+    assert L.tj_quad_apply(16, 16, 16, _lib.TJ_F32, 0, 128, 64, 64, st, ss, st, None) == _lib.TJ_OK
+    assert L.tj_quad_apply(8, 16, 16, _lib.TJ_F32, 2, 128, 64, 64, st, ss, st, None) == _lib.TJ_ERR_ALIGN
+    assert L.tj_quad_apply(16, 16, 16, _lib.TJ_F32, 2, 128, 64, 64, _s3(128 * 64, 65, 1), ss, st, None) == _lib.TJ_ERR_ALIGN
+    assert L.tj_quad_update(16, 16, 16, None, 2, 128, 64, 32, st, st, ss, None, None) == _lib.TJ_ERR_UNSUPPORTED
+    assert L.tj_quad_update(16, 16, 16, None, 2, 128, 64, 64, st, st, _s3(4096 * 64, 64, 2), None, None) == _lib.TJ_ERR_ALIGN
+    assert L.tj_quad_update(16, 16, 16, 24, 2, 128, 64, 64, st, st, ss, ss, None) == _lib.TJ_ERR_ALIGN
+    assert L.tj_causal_diag(16, 16, 16, 16, 16, 2, 128, 64, 64, st, st, st, st, 127, None) == _lib.TJ_ERR_SHAPE
+    assert L.tj_causal_diag(16, 16, 16, 16, None, 2, 128, 64, 64, st, st, st, st, 128, None) == _lib.TJ_ERR_ALIGN
+    assert L.tj_causal_diag(16, 16, 16, 16, 16, 2, 128, 48, 64, st, st, st, st, 128, None) == _lib.TJ_ERR_UNSUPPORTED
+
+
+def test_poly_parts_refuse_cpu_tensors():
+    import torch
+
+    from techjam_amd.errors import UnsupportedCaseError
+    from techjam_amd.kernels.poly_parts import causal_diag, quad_apply, quad_update
+
+    a = torch.zeros(2, 128, 64, dtype=torch.float16)
+    with pytest.raises(UnsupportedCaseError):
+        quad_apply(a, torch.zeros(2, 4096, 64))
+    with pytest.raises(UnsupportedCaseError):
+        quad_update(a, a, torch.zeros(2, 4096, 64))
+    with pytest.raises(UnsupportedCaseError):
+        causal_diag(a, a, a)
