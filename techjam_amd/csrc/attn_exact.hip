@@ -228,10 +228,16 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
 
   float16_t oacc[QB][TL::DB];
   float m_run[QB], l_run[QB];
+  // -m_run splat kept as a register block: it is the C operand of each query
+  // block's first score MFMA, so the scores leave the MFMA already shifted
+  // without re-initialising the accumulators every tile.
+  float16_t cneg[QB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     m_run[qb] = -__builtin_inff();
     l_run[qb] = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) cneg[qb][r] = 0.f;
 #pragma unroll
     for (int db = 0; db < TL::DB; ++db)
 #pragma unroll
@@ -257,14 +263,6 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
       const bool first = kv0 == 0;
       float16_t sacc[QB][2];
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
-        const float c_init = first ? 0.f : -m_run[qb];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) sacc[qb][kb][r] = c_init;
-      }
-#pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int ks = 0; ks < TL::KS; ++ks) {
@@ -273,12 +271,15 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
             const half8_t kl = *reinterpret_cast<const half8_t*>(&sm.klo[cur][kb * 32 + ln][16 * ks + 8 * hl]);
 #pragma unroll
             for (int qb = 0; qb < QB; ++qb) {
-              sacc[qb][kb] = mfma32(kl, qf[qb][ks], sacc[qb][kb]);
+              sacc[qb][kb] = mfma32(kl, qf[qb][ks], ks == 0 ? cneg[qb] : sacc[qb][kb]);
               sacc[qb][kb] = mfma32(kf, qlo[qb][ks], sacc[qb][kb]);
             }
-          }
 #pragma unroll
-          for (int qb = 0; qb < QB; ++qb) sacc[qb][kb] = mfma32(kf, qf[qb][ks], sacc[qb][kb]);
+            for (int qb = 0; qb < QB; ++qb) sacc[qb][kb] = mfma32(kf, qf[qb][ks], sacc[qb][kb]);
+          } else {
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb) sacc[qb][kb] = mfma32(kf, qf[qb][ks], ks == 0 ? cneg[qb] : sacc[qb][kb]);
+          }
         }
 
       half8_t pf[QB][4];
@@ -320,6 +321,8 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
           for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) sacc[qb][kb][r] -= shift;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) cneg[qb][r] = -m_run[qb];
         }
         // P = exp2(S) rounded to fp16; the row sum adds the same rounded values.
 #pragma unroll
