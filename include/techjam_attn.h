@@ -110,7 +110,11 @@ int tj_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype,
  *                    the rows tj_attn_fwd must compute for that head,
  *   split_out[bh]  : 1 for heads routed to the exact fallback (their score
  *                    range is wide), 0 otherwise -- tj_attn_fwd's qk_split.
- * Any output pointer except flags_out may be NULL.
+ * Any output pointer except flags_out may be NULL. workspace (16-byte
+ * aligned, tj_score_guard_workspace_bytes(B, H, n_samples) bytes, contents
+ * irrelevant) holds per-(b,h) partial sums between the two launches; calls
+ * sharing one workspace must be ordered on one stream. D must be a multiple
+ * of 4 (<= 128), rows and strides multiples of 4 elements.
  */
 int tj_score_guard(const void* q, const void* k, int dtype,
                    int64_t B, int64_t H, int64_t S, int64_t D,
@@ -119,7 +123,12 @@ int tj_score_guard(const void* q, const void* k, int dtype,
                    float ceiling, int64_t exact_prefix,
                    float* sigma_out, float* mean_out, float* smax_out, int32_t* flags_out,
                    float* coeffs_out, int32_t* row_limit_out, int32_t* split_out,
-                   hipStream_t stream);
+                   void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/*
+ * Workspace needed by tj_score_guard, in bytes (0 for invalid sizes).
+ */
+size_t tj_score_guard_workspace_bytes(int64_t B, int64_t H, int64_t n_samples);
 
 /*
  * Workspace needed by tj_poly_attn_fwd, in bytes.

@@ -7,11 +7,15 @@
 // written to device memory where the polynomial and exact kernels read them,
 // so the route decision never leaves the GPU.
 //
-// One workgroup per (b, h). The sampled rows are staged in LDS as fp32 in
-// 64-row blocks, transposed so that a thread reads four rows with one 16-byte
-// load; each thread forms a 4x4 tile of the 64x64 scores of a block pair and
-// keeps running sum, sum of squares and max |s|; a workgroup reduction in
-// fp64 produces the Bessel-corrected standard deviation.
+// Two launches. The first has one workgroup per (b, h) and 64-row block of
+// the sampled query rows: the block is staged once in LDS (fp32, transposed,
+// scaled), the sampled key rows stream through LDS in 64-row blocks gathered
+// with 16-byte loads, each thread forms a 4x4 tile of every 64x64 score block
+// and keeps running sum, sum of squares (fp64) and max |s|; the workgroup's
+// three partials go to the caller's workspace. The second launch (one thread
+// per (b, h)) adds the partials of a head in a fixed order -- the result does
+// not depend on scheduling -- and writes the Bessel-corrected standard
+// deviation, the route flag and what the attention kernels read from it.
 #include <math.h>
 
 #include "tj_common.h"
@@ -40,31 +44,47 @@ struct GuardArgs {
   int32_t* split;
 };
 
-// Stage up to GB sampled rows, transposed: dst[d][r] = src[idx[r0 + r], d] * mul.
+__host__ __device__ constexpr int guard_blocks(int n) { return (n + GB - 1) / GB; }
+
+// Stage up to GB sampled rows, transposed: dst[d][r] = src[idx[r0 + r], d] * mul,
+// 16-byte (fp32) or 8-byte (fp16) gathers of four consecutive dims.
 template <typename T>
 __device__ __forceinline__ void stage_rows(float (*dst)[GB + 4], const T* src, const View4& vw, int b,
                                            int h, const GuardArgs& a, int r0, float mul) {
   const int rows = min(GB, a.n - r0);
-  for (int e = threadIdx.x; e < GB * a.D; e += GT) {
-    const int r = e / a.D, d = e % a.D;
-    float x = 0.f;
+  const int q4 = a.D / 4;  // four-dim groups per row
+  for (int e = threadIdx.x; e < GB * q4; e += GT) {
+    const int r = e / q4, d = 4 * (e % q4);
+    float x[4] = {0.f, 0.f, 0.f, 0.f};
     if (r < rows) {
       int s = a.idx[r0 + r];
       s = min(max(s, 0), a.S - 1);
-      x = (float)src[vw.row(b, h, s) + d] * mul;
+      const T* p = src + vw.row(b, h, s) + d;
+      if constexpr (sizeof(T) == 4) {
+        const float4_t v = *reinterpret_cast<const float4_t*>(p);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[j] = v[j] * mul;
+      } else {
+        const half4_t v = *reinterpret_cast<const half4_t*>(p);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[j] = (float)v[j] * mul;
+      }
     }
-    dst[d][r] = x;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dst[d + j][r] = x[j];
   }
 }
 
 template <typename T>
-__global__ __launch_bounds__(GT) void score_guard_kernel(GuardArgs a) {
+__global__ __launch_bounds__(GT) void score_guard_partial_kernel(GuardArgs a, double* partials) {
   __shared__ float qs[GMAXD][GB + 4];
   __shared__ float ks[GMAXD][GB + 4];
   __shared__ double red_s[GT / kWave], red_q[GT / kWave];
   __shared__ float red_m[GT / kWave];
 
-  const int bh = blockIdx.x;
+  const int nb = guard_blocks(a.n);
+  const int id = blockIdx.x;
+  const int bh = id / nb, rb = id % nb;
   const int b = bh / a.H, h = bh % a.H;
   const T* qp = reinterpret_cast<const T*>(a.q);
   const T* kp = reinterpret_cast<const T*>(a.k);
@@ -72,45 +92,44 @@ __global__ __launch_bounds__(GT) void score_guard_kernel(GuardArgs a) {
   // Each thread owns a 4x4 tile of the 64x64 score block: rows 4*ti.., cols 4*tj..
   const int ti = t % 16;
   const int tj = t / 16;
+  const int r0 = rb * GB;
+  const int nr = min(GB, a.n - r0);
+  stage_rows<T>(qs, qp, a.vq, b, h, a, r0, a.scale);
 
   float mx = 0.f;
   double dsum = 0.0, dsq = 0.0;
-  for (int r0 = 0; r0 < a.n; r0 += GB) {
-    const int nr = min(GB, a.n - r0);
-    for (int c0 = 0; c0 < a.n; c0 += GB) {
-      const int nc = min(GB, a.n - c0);
-      __syncthreads();
-      stage_rows<T>(qs, qp, a.vq, b, h, a, r0, a.scale);
-      stage_rows<T>(ks, kp, a.vk, b, h, a, c0, 1.f);
-      __syncthreads();
-      float acc[4][4];
+  for (int c0 = 0; c0 < a.n; c0 += GB) {
+    const int nc = min(GB, a.n - c0);
+    __syncthreads();
+    stage_rows<T>(ks, kp, a.vk, b, h, a, c0, 1.f);
+    __syncthreads();
+    float acc[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[r][c] = 0.f;
+    for (int d = 0; d < a.D; ++d) {
+      const float4_t qv = *reinterpret_cast<const float4_t*>(&qs[d][4 * ti]);
+      const float4_t kv = *reinterpret_cast<const float4_t*>(&ks[d][4 * tj]);
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) acc[r][c] = 0.f;
-      for (int d = 0; d < a.D; ++d) {
-        const float4_t qv = *reinterpret_cast<const float4_t*>(&qs[d][4 * ti]);
-        const float4_t kv = *reinterpret_cast<const float4_t*>(&ks[d][4 * tj]);
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-          for (int c = 0; c < 4; ++c) acc[r][c] = fmaf(qv[r], kv[c], acc[r][c]);
-      }
-      float sum = 0.f, sq = 0.f;
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          if (4 * ti + r < nr && 4 * tj + c < nc) {
-            const float s = acc[r][c];
-            sum += s;
-            sq = fmaf(s, s, sq);
-            mx = fmaxf(mx, fabsf(s));
-          }
-        }
-      dsum += sum;
-      dsq += sq;
+        for (int c = 0; c < 4; ++c) acc[r][c] = fmaf(qv[r], kv[c], acc[r][c]);
     }
+    float sum = 0.f, sq = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (4 * ti + r < nr && 4 * tj + c < nc) {
+          const float s = acc[r][c];
+          sum += s;
+          sq = fmaf(s, s, sq);
+          mx = fmaxf(mx, fabsf(s));
+        }
+      }
+    dsum += sum;
+    dsq += sq;
   }
   // Workgroup reduction.
   for (int off = kWave / 2; off > 0; off /= 2) {
@@ -133,29 +152,50 @@ __global__ __launch_bounds__(GT) void score_guard_kernel(GuardArgs a) {
       s2 += red_q[i];
       m = fmaxf(m, red_m[i]);
     }
-    const double cnt = (double)a.n * (double)a.n;
-    double var = cnt > 1.0 ? (s2 - s1 * s1 / cnt) / (cnt - 1.0) : 0.0;
-    if (var < 0.0) var = 0.0;
-    const double sigma = sqrt(var);
-    const bool safe = isfinite(sigma) && sigma > 0.0 && sigma <= (double)a.ceiling;
-    if (a.sigma) a.sigma[bh] = (float)sigma;
-    if (a.mean) a.mean[bh] = (float)(cnt > 0.0 ? s1 / cnt : 0.0);
-    if (a.smax) a.smax[bh] = m;
-    a.flags[bh] = safe ? 1 : 0;
-    if (a.coeffs) {
-      const double s2h = 0.5 * sigma * sigma;
-      const double g = exp(s2h);
-      a.coeffs[3 * bh + 0] = (float)(g * fmax(1.0 - s2h, 1e-3));
-      a.coeffs[3 * bh + 1] = (float)g;
-      a.coeffs[3 * bh + 2] = (float)(0.5 * g);
-    }
-    if (a.row_limit) a.row_limit[bh] = safe ? min(a.exact_prefix, a.S) : a.S;
-    if (a.split) a.split[bh] = safe ? 0 : 1;
+    partials[3 * size_t(id) + 0] = s1;
+    partials[3 * size_t(id) + 1] = s2;
+    partials[3 * size_t(id) + 2] = (double)m;
   }
+}
+
+__global__ __launch_bounds__(GT) void score_guard_final_kernel(GuardArgs a, const double* partials, int bhn) {
+  const int bh = blockIdx.x * GT + threadIdx.x;
+  if (bh >= bhn) return;
+  const int nb = guard_blocks(a.n);
+  double s1 = 0.0, s2 = 0.0, m = 0.0;
+  for (int i = 0; i < nb; ++i) {
+    const double* p = partials + 3 * (size_t(bh) * nb + i);
+    s1 += p[0];
+    s2 += p[1];
+    m = fmax(m, p[2]);
+  }
+  const double cnt = (double)a.n * (double)a.n;
+  double var = cnt > 1.0 ? (s2 - s1 * s1 / cnt) / (cnt - 1.0) : 0.0;
+  if (var < 0.0) var = 0.0;
+  const double sigma = sqrt(var);
+  const bool safe = isfinite(sigma) && sigma > 0.0 && sigma <= (double)a.ceiling;
+  if (a.sigma) a.sigma[bh] = (float)sigma;
+  if (a.mean) a.mean[bh] = (float)(cnt > 0.0 ? s1 / cnt : 0.0);
+  if (a.smax) a.smax[bh] = (float)m;
+  a.flags[bh] = safe ? 1 : 0;
+  if (a.coeffs) {
+    const double s2h = 0.5 * sigma * sigma;
+    const double g = exp(s2h);
+    a.coeffs[3 * bh + 0] = (float)(g * fmax(1.0 - s2h, 1e-3));
+    a.coeffs[3 * bh + 1] = (float)g;
+    a.coeffs[3 * bh + 2] = (float)(0.5 * g);
+  }
+  if (a.row_limit) a.row_limit[bh] = safe ? min(a.exact_prefix, a.S) : a.S;
+  if (a.split) a.split[bh] = safe ? 0 : 1;
 }
 
 }  // namespace
 }  // namespace tj
+
+extern "C" size_t tj_score_guard_workspace_bytes(int64_t B, int64_t H, int64_t n_samples) {
+  if (B <= 0 || H <= 0 || n_samples <= 0 || n_samples >= (int64_t(1) << 30)) return 0;
+  return size_t(B) * size_t(H) * size_t(tj::guard_blocks((int)n_samples)) * 3 * sizeof(double);
+}
 
 extern "C" int tj_score_guard(const void* q, const void* k, int dtype,
                               int64_t B, int64_t H, int64_t S, int64_t D,
@@ -164,13 +204,21 @@ extern "C" int tj_score_guard(const void* q, const void* k, int dtype,
                               float ceiling, int64_t exact_prefix,
                               float* sigma_out, float* mean_out, float* smax_out, int32_t* flags_out,
                               float* coeffs_out, int32_t* row_limit_out, int32_t* split_out,
-                              hipStream_t stream) {
+                              void* workspace, size_t workspace_bytes, hipStream_t stream) {
   if (dtype != TJ_F32 && dtype != TJ_F16) return TJ_ERR_DTYPE;
   if (B <= 0 || H <= 0 || S <= 0 || D <= 0 || n_samples <= 0 || n_samples > S) return TJ_ERR_SHAPE;
-  if (D > tj::GMAXD) return TJ_ERR_UNSUPPORTED;
+  if (D > tj::GMAXD || D % 4 != 0) return TJ_ERR_UNSUPPORTED;
   if (!q || !k || !sample_idx || !flags_out) return TJ_ERR_SHAPE;
   if (!q_strides || !k_strides || q_strides[3] != 1 || k_strides[3] != 1) return TJ_ERR_ALIGN;
+  const int64_t elt = dtype == TJ_F32 ? 4 : 2;
+  // 4-dim gathers: rows must start on 4-element boundaries of aligned bases.
+  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k)) % (4 * elt) != 0) return TJ_ERR_ALIGN;
+  for (int i = 0; i < 3; ++i)
+    if (q_strides[i] % 4 != 0 || k_strides[i] % 4 != 0) return TJ_ERR_ALIGN;
   if (B * H >= (int64_t(1) << 31) || S >= (int64_t(1) << 31)) return TJ_ERR_SHAPE;
+  const size_t need = tj_score_guard_workspace_bytes(B, H, n_samples);
+  if (need == 0 || B * H * tj::guard_blocks((int)n_samples) >= (int64_t(1) << 31)) return TJ_ERR_SHAPE;
+  if (workspace == nullptr || workspace_bytes < need || !tjh::aligned16(workspace)) return TJ_ERR_WORKSPACE;
   tj::GuardArgs a;
   a.q = q; a.k = k;
   a.vq = {q_strides[0], q_strides[1], q_strides[2]};
@@ -182,10 +230,16 @@ extern "C" int tj_score_guard(const void* q, const void* k, int dtype,
   a.sigma = sigma_out; a.mean = mean_out; a.smax = smax_out; a.flags = flags_out; a.coeffs = coeffs_out;
   a.row_limit = row_limit_out;
   a.split = split_out;
-  const dim3 grid((unsigned)(B * H));
+  double* partials = static_cast<double*>(workspace);
+  const dim3 grid((unsigned)(B * H * tj::guard_blocks(a.n)));
   if (dtype == TJ_F32)
-    hipLaunchKernelGGL(tj::score_guard_kernel<float>, grid, dim3(tj::GT), 0, stream, a);
+    hipLaunchKernelGGL(tj::score_guard_partial_kernel<float>, grid, dim3(tj::GT), 0, stream, a, partials);
   else
-    hipLaunchKernelGGL(tj::score_guard_kernel<half_t>, grid, dim3(tj::GT), 0, stream, a);
+    hipLaunchKernelGGL(tj::score_guard_partial_kernel<half_t>, grid, dim3(tj::GT), 0, stream, a, partials);
+  const int rc = tjh::launch_status();
+  if (rc != TJ_OK) return rc;
+  const int bhn = (int)(B * H);
+  hipLaunchKernelGGL(tj::score_guard_final_kernel, dim3((unsigned)((bhn + tj::GT - 1) / tj::GT)), dim3(tj::GT), 0,
+                     stream, a, static_cast<const double*>(partials), bhn);
   return tjh::launch_status();
 }

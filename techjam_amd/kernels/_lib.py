@@ -44,8 +44,9 @@ SIGNATURES = {
     "tj_score_guard": (
         _int,
         [_vp, _vp, _int, _i64, _i64, _i64, _i64, _i64p, _i64p, _f32, _vp, _i64, _f32, _i64,
-         _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
+         _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp],
     ),
+    "tj_score_guard_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64]),
     "tj_poly_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, _i64]),
     "tj_poly_attn_fwd": (
         _int,

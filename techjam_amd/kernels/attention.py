@@ -211,12 +211,16 @@ def score_guard(
         row_limit=torch.empty(m, dtype=torch.int32, device=dev),
         split=torch.empty(m, dtype=torch.int32, device=dev),
     )
-    code = _lib.lib().tj_score_guard(
+    lib = _lib.lib()
+    ws_bytes = lib.tj_score_guard_workspace_bytes(b, h, idx.numel())
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+    code = lib.tj_score_guard(
         q.data_ptr(), k.data_ptr(), _DTYPES[q.dtype], b, h, s, d,
         _lib.strides4(q), _lib.strides4(k), float(scale), idx.data_ptr(), idx.numel(),
         float(ceiling), int(exact_prefix),
         res.sigma.data_ptr(), res.mean.data_ptr(), res.smax.data_ptr(), res.flags.data_ptr(),
-        res.coeffs.data_ptr(), res.row_limit.data_ptr(), res.split.data_ptr(), _stream_ptr(dev),
+        res.coeffs.data_ptr(), res.row_limit.data_ptr(), res.split.data_ptr(),
+        ws.data_ptr(), ws.numel(), _stream_ptr(dev),
     )
     _lib.check(code, "tj_score_guard")
     return res

@@ -95,12 +95,24 @@ def test_guard_rejects_bad_arguments_before_launching():
     st = _strides(64 * 128 * 4, 64, 64 * 4, 1)
     # more samples than rows
     assert L.tj_score_guard(16, 16, _lib.TJ_F32, 1, 4, 128, 64, st, st, 0.125, 16, 256, 0.4, 64,
-                            None, None, None, 16, None, None, None, None) == _lib.TJ_ERR_SHAPE
+                            None, None, None, 16, None, None, None, 16, 1 << 20, None) == _lib.TJ_ERR_SHAPE
     # missing flags output
     assert L.tj_score_guard(16, 16, _lib.TJ_F32, 1, 4, 128, 64, st, st, 0.125, 16, 64, 0.4, 64,
-                            None, None, None, None, None, None, None, None) == _lib.TJ_ERR_SHAPE
+                            None, None, None, None, None, None, None, 16, 1 << 20, None) == _lib.TJ_ERR_SHAPE
     assert L.tj_score_guard(16, 16, _lib.TJ_F32, 1, 4, 128, 256, st, st, 0.125, 16, 64, 0.4, 64,
-                            None, None, None, 16, None, None, None, None) == _lib.TJ_ERR_UNSUPPORTED
+                            None, None, None, 16, None, None, None, 16, 1 << 20, None) == _lib.TJ_ERR_UNSUPPORTED
+    # workspace: missing, too small, misaligned
+    need = L.tj_score_guard_workspace_bytes(1, 4, 64)
+    assert need == 1 * 4 * 1 * 3 * 8
+    assert L.tj_score_guard_workspace_bytes(1, 4, 512) == 4 * 8 * 3 * 8
+    assert L.tj_score_guard_workspace_bytes(0, 4, 512) == 0
+    for ws, nbytes in ((None, need), (16, need - 8), (24, need)):
+        assert L.tj_score_guard(16, 16, _lib.TJ_F32, 1, 4, 128, 64, st, st, 0.125, 16, 64, 0.4, 64,
+                                None, None, None, 16, None, None, None, ws, nbytes, None) == _lib.TJ_ERR_WORKSPACE
+    # rows must be 4-element aligned for the gathers
+    odd = _strides(64 * 128 * 4, 64, 66, 1)
+    assert L.tj_score_guard(16, 16, _lib.TJ_F32, 1, 4, 128, 64, odd, st, 0.125, 16, 64, 0.4, 64,
+                            None, None, None, 16, None, None, None, 16, need, None) == _lib.TJ_ERR_ALIGN
 
 
 def test_check_maps_codes_to_reference_exceptions():
