@@ -49,6 +49,10 @@ def parse_args():
                    choices=["attn-core", "extreme", "model-c1", "model-c2", "model-c4", "copy-1gib"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-repeats", type=int, default=3)
+    # Float32 GEMM flags of the model workloads; the defaults are the reference
+    # harness's validated contract (src/benchmark.py:133-141, src/dispatcher.py:69-70).
+    p.add_argument("--matmul-precision", choices=("highest", "high", "medium"), default="high")
+    p.add_argument("--allow-tf32", action=argparse.BooleanOptionalAction, default=True)
     return p.parse_args()
 
 
@@ -145,6 +149,8 @@ def model(name):
                                        c.padding_ratio, 1.0)
         x, mask = x.to(dev), mask.to(dev)
         lengths = mask.sum(1).tolist()
+        torch.set_float32_matmul_precision(args.matmul_precision)
+        torch.backends.cuda.matmul.allow_tf32 = args.allow_tf32
 
         def step():
             with torch.inference_mode():
@@ -155,7 +161,9 @@ def model(name):
         config = {"workload": f"{c.num_layers}-layer encoder {name}: {c.description}",
                   "batch": c.batch_size, "seq_len": c.seq_len, "d_model": c.d_model,
                   "heads": c.num_heads, "ffn_dim": c.ffn_dim, "layers": c.num_layers,
-                  "roofline_scope": "attention FLOPs over the whole forward (GEMMs not counted)"}
+                  "roofline_scope": "attention FLOPs over the whole forward (GEMMs not counted)",
+                  "gemm": f"hipBLASLt, fp32 tensors, matmul precision {args.matmul_precision!r}, "
+                          f"allow_tf32={args.allow_tf32}"}
         return step, c.batch_size * c.seq_len, flops, 0.0, config, f"model_{name.lower()}.md"
     return build
 

@@ -23,10 +23,9 @@ from __future__ import annotations
 from typing import Optional
 
 import torch
-import torch.nn.functional as F
 
 from ..kernels.attention import scaled_dot_product_attention
-from ..model import HipSelfAttention
+from ..model import HipSelfAttention, linear
 
 
 class StridedSDPASelfAttention(HipSelfAttention):
@@ -83,7 +82,7 @@ class PackedQKVSDPASelfAttention(StridedSDPASelfAttention):
             # The packed buffers are inference caches, not trainable parameters.
             return super().project_qkv(x)
         b, s, _ = x.shape
-        packed = F.linear(x, self._packed_qkv_weight, self._packed_qkv_bias)
+        packed = linear(x, self._packed_qkv_weight, self._packed_qkv_bias)
         q, k, v = packed.view(b, s, 3, self.num_heads, self.head_dim).unbind(dim=2)
         return q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
 

@@ -4,8 +4,9 @@ Same module tree, parameter names and construction order as the reference
 model (``torch_transformer_benchmark.py:29-172``), so the harness's strict
 ``load_state_dict`` works unchanged and a seeded construction gives the same
 weights. Only the attention module differs: ``HipSelfAttention`` projects with
-``nn.Linear`` (hipBLASLt GEMMs) and calls the gfx950 attention kernel through
-the C ABI instead of materialising a score tensor.
+hipBLASLt GEMMs (``Linear``, an ``nn.Linear`` whose bias add stays outside the
+GEMM when the fast float32 matmul mode is on) and calls the gfx950 attention
+kernel through the C ABI instead of materialising a score tensor.
 """
 
 from __future__ import annotations
@@ -48,6 +49,27 @@ def config_key(config) -> tuple:
             config.ffn_dim, config.causal, config.num_layers)
 
 
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor]) -> torch.Tensor:
+    """``F.linear``; when float32 matmuls may use the faster hipBLASLt mode
+    (``torch.get_float32_matmul_precision() != "highest"``, the reference
+    harness's validated setting) the bias is added after a bias-free GEMM,
+    because the fused-bias GEMM ignores that mode on this stack (16384x1024 by
+    1024x3072: 0.72 ms fused either way, 0.29 ms bias-free in the fast mode)."""
+    if bias is None or x.device.type != "cuda" or torch.get_float32_matmul_precision() == "highest":
+        return F.linear(x, weight, bias)
+    y = F.linear(x, weight)
+    y += bias
+    return y
+
+
+class Linear(nn.Linear):
+    """``nn.Linear`` with the same parameters and state-dict names whose
+    forward is :func:`linear`."""
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return linear(x, self.weight, self.bias)
+
+
 class HipSelfAttention(nn.Module):
     """Multi-head self-attention: Linear projections + the HIP exact kernel.
 
@@ -65,10 +87,10 @@ class HipSelfAttention(nn.Module):
         self.num_heads = num_heads
         self.head_dim = d_model // num_heads
         self.scale = self.head_dim ** -0.5
-        self.q_proj = nn.Linear(d_model, d_model)
-        self.k_proj = nn.Linear(d_model, d_model)
-        self.v_proj = nn.Linear(d_model, d_model)
-        self.out_proj = nn.Linear(d_model, d_model)
+        self.q_proj = Linear(d_model, d_model)
+        self.k_proj = Linear(d_model, d_model)
+        self.v_proj = Linear(d_model, d_model)
+        self.out_proj = Linear(d_model, d_model)
 
     def heads_view(self, t: torch.Tensor) -> torch.Tensor:
         """``[B, S, D] -> [B, H, S, dh]`` as a strided view (no copy)."""
@@ -99,8 +121,8 @@ class EncoderBlock(nn.Module):
         self.norm1 = nn.LayerNorm(d_model)
         self.attention = HipSelfAttention(d_model, num_heads)
         self.norm2 = nn.LayerNorm(d_model)
-        self.ffn_in = nn.Linear(d_model, ffn_dim)
-        self.ffn_out = nn.Linear(ffn_dim, d_model)
+        self.ffn_in = Linear(d_model, ffn_dim)
+        self.ffn_out = Linear(ffn_dim, d_model)
 
     def forward(self, x, valid_token_mask, causal, valid_len=None):
         x = x + self.attention(self.norm1(x), valid_token_mask, causal, valid_len=valid_len)

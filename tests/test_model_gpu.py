@@ -11,6 +11,8 @@ zero failing elements.
 
 from __future__ import annotations
 
+import contextlib
+
 import pytest
 import torch
 
@@ -31,10 +33,28 @@ def _pair(cfg: OracleConfig, seed: int, device):
     return base, cand.to(device)
 
 
-def _check(cfg, seeds, padding, cuda, oracle_on_gpu=False, oracle_cls=DenseTransformer):
+@contextlib.contextmanager
+def _matmul_flags(precision: str, allow_tf32: bool):
+    """Scoped float32-matmul flags (they are process-global in torch)."""
+    old = (torch.get_float32_matmul_precision(), torch.backends.cuda.matmul.allow_tf32)
+    torch.set_float32_matmul_precision(precision)
+    torch.backends.cuda.matmul.allow_tf32 = allow_tf32
+    try:
+        yield
+    finally:
+        torch.set_float32_matmul_precision(old[0])
+        torch.backends.cuda.matmul.allow_tf32 = old[1]
+
+
+def _check(cfg, seeds, padding, cuda, oracle_on_gpu=False, oracle_cls=DenseTransformer, harness_flags=False):
+    """``harness_flags``: run the candidate under the reference harness's
+    validated numerics flags (matmul precision "high", TF32 allowed;
+    src/benchmark.py:133-141, src/dispatcher.py:69-70) while the oracle keeps
+    full fp32 GEMMs."""
     from techjam_amd import dispatcher as D
 
     torch.backends.cuda.matmul.allow_tf32 = False
+    cand_flags = ("high", True) if harness_flags else ("highest", False)
     base, cand = _pair(cfg, 4321, cuda)
     if oracle_cls is not DenseTransformer:
         lm = oracle_cls(cfg).eval()
@@ -45,9 +65,11 @@ def _check(cfg, seeds, padding, cuda, oracle_on_gpu=False, oracle_cls=DenseTrans
     for seed in seeds:
         x, mask = generate_random_case(cfg, torch.device("cpu"), torch.float32, seed, padding, 1.0)
         with torch.inference_mode():
-            ref = base(x.to(cuda), mask.to(cuda)).cpu() if oracle_on_gpu else base(x, mask)
-            got = cand(x.to(cuda), mask.to(cuda))
-            torch.cuda.synchronize()
+            with _matmul_flags("highest", False):
+                ref = base(x.to(cuda), mask.to(cuda)).cpu() if oracle_on_gpu else base(x, mask)
+            with _matmul_flags(*cand_flags):
+                got = cand(x.to(cuda), mask.to(cuda))
+                torch.cuda.synchronize()
         res = compare_outputs(ref, got.cpu(), rtol=0.02, atol=0.002)
         print(f"seed {seed}: max_abs={res.max_abs_error:.3e} failed={res.failed_elements}/{res.total_elements}")
         assert res.passed, f"seed {seed}: {res.failed_elements} failed, max_abs {res.max_abs_error:.3e}"
@@ -71,6 +93,16 @@ def test_official_cases_with_supported_head_dims(cuda, case_id):
     c = load_official_cases()[case_id]
     cfg = OracleConfig(c.batch_size, c.seq_len, c.qkv_dim, c.heads, c.ffn_dim, c.layers, c.causal)
     _check(cfg, (1234,), 0.3, cuda)
+
+
+def test_config_2_under_the_reference_harness_matmul_flags(cuda):
+    cfg = OracleConfig(8, 1024, 512, 8, 2048, 4, True)
+    _check(cfg, (1234,), 0.5, cuda, harness_flags=True)
+
+
+def test_config_4_under_the_reference_harness_matmul_flags(cuda):
+    cfg = OracleConfig(2, 8192, 1024, 16, 4096, 4, True)
+    _check(cfg, (1234,), 0.5, cuda, oracle_on_gpu=True, oracle_cls=LinearMemoryReference, harness_flags=True)
 
 
 def test_non_causal_right_padded_model(cuda):
