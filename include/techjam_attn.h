@@ -205,6 +205,27 @@ int tj_causal_diag(const void* a, const void* b, const void* v, float* num, floa
                    const int64_t b_strides[3], const int64_t v_strides[3],
                    const int64_t num_strides[3], int64_t den_stride_m, hipStream_t stream);
 
+/*
+ * Fused tails of the encoder block (replaces the bias add, residual add and
+ * masked_fill of torch_transformer_benchmark.py:116-121 and :140-145 around a
+ * bias-free projection GEMM). fp32 [rows, cols] row-major, cols % 4 == 0,
+ * 16-byte aligned; rows = B * seq_len, row b*seq_len+s valid iff
+ * s < valid_len[b] (valid_len NULL: every row valid).
+ *   mode 0: out = x + y + bias
+ *   mode 1: out = x + (valid ? y + bias : 0)    (attention output, then residual)
+ *   mode 2: out = valid ? x + y + bias : 0      (FFN output, residual, row zeroing)
+ * out may alias x or y.
+ */
+int tj_bias_residual(float* out, const float* x, const float* y, const float* bias,
+                     int64_t rows, int64_t cols, int64_t seq_len, const int32_t* valid_len,
+                     int mode, hipStream_t stream);
+
+/*
+ * y = gelu(y + bias) in place, exact (erf) GELU -- the bias of the FFN input
+ * GEMM fused with F.gelu(approximate="none") (torch_transformer_benchmark.py:145).
+ */
+int tj_bias_gelu(float* y, const float* bias, int64_t rows, int64_t cols, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,91 @@
+// Fused elementwise tails of the encoder block (torch_transformer_benchmark.py:
+// 116-121, 140-145): the bias of a bias-free projection GEMM, the residual add,
+// exact GELU and the zeroing of padded rows, each done in one pass over the
+// activation instead of two or three.
+//
+//   tj_bias_residual : out = x + (row valid ? y + b : 0)          (mode 1)
+//                      out = row valid ? x + y + b : 0             (mode 2)
+//                      out = x + y + b                             (mode 0)
+//   tj_bias_gelu     : y = gelu(y + b), exact (erf) form, in place
+//
+// Tensors are fp32 [rows, cols] row-major with cols % 4 == 0 and 16-byte
+// aligned bases; row r = b * seq_len + s is valid iff s < valid_len[b].
+#include "tj_common.h"
+
+namespace tj {
+namespace {
+
+constexpr int ET = 256;
+
+__device__ __forceinline__ bool row_valid(int64_t row, int64_t seq_len, const int32_t* valid_len) {
+  if (valid_len == nullptr) return true;
+  const int64_t b = row / seq_len, s = row % seq_len;
+  return s < (int64_t)valid_len[b];
+}
+
+__global__ __launch_bounds__(ET) void bias_residual_kernel(float* out, const float* x, const float* y, const float* bias,
+                                                           int64_t n4, int64_t c4, int64_t seq_len,
+                                                           const int32_t* valid_len, int mode) {
+  for (int64_t i = blockIdx.x * (int64_t)ET + threadIdx.x; i < n4; i += (int64_t)gridDim.x * ET) {
+    const int64_t row = i / c4, c = i % c4;
+    const float4_t xv = reinterpret_cast<const float4_t*>(x)[i];
+    const float4_t yv = reinterpret_cast<const float4_t*>(y)[i];
+    const float4_t bv = reinterpret_cast<const float4_t*>(bias)[c];
+    const bool ok = mode == 0 || row_valid(row, seq_len, valid_len);
+    float4_t r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float t = yv[e] + bv[e];
+      r[e] = mode == 2 ? (ok ? xv[e] + t : 0.f) : xv[e] + (ok ? t : 0.f);
+    }
+    reinterpret_cast<float4_t*>(out)[i] = r;
+  }
+}
+
+__global__ __launch_bounds__(ET) void bias_gelu_kernel(float* y, const float* bias, int64_t n4, int64_t c4) {
+  for (int64_t i = blockIdx.x * (int64_t)ET + threadIdx.x; i < n4; i += (int64_t)gridDim.x * ET) {
+    const int64_t c = i % c4;
+    float4_t v = reinterpret_cast<const float4_t*>(y)[i];
+    const float4_t bv = reinterpret_cast<const float4_t*>(bias)[c];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float t = v[e] + bv[e];
+      v[e] = 0.5f * t * (1.f + erff(t * 0.70710678118654752f));
+    }
+    reinterpret_cast<float4_t*>(y)[i] = v;
+  }
+}
+
+unsigned grid_for(int64_t n4) {
+  const int64_t blocks = (n4 + ET - 1) / ET;
+  return (unsigned)(blocks < 256 * 32 ? blocks : 256 * 32);
+}
+
+}  // namespace
+}  // namespace tj
+
+extern "C" int tj_bias_residual(float* out, const float* x, const float* y, const float* bias, int64_t rows,
+                                int64_t cols, int64_t seq_len, const int32_t* valid_len, int mode,
+                                hipStream_t stream) {
+  if (rows < 0 || cols <= 0 || seq_len <= 0 || mode < 0 || mode > 2) return TJ_ERR_SHAPE;
+  if (mode != 0 && valid_len != nullptr && rows % seq_len != 0) return TJ_ERR_SHAPE;
+  if (cols % 4 != 0) return TJ_ERR_UNSUPPORTED;
+  if (rows == 0) return TJ_OK;
+  if (!out || !x || !y || !bias) return TJ_ERR_SHAPE;
+  if (!tjh::aligned16(out) || !tjh::aligned16(x) || !tjh::aligned16(y) || !tjh::aligned16(bias)) return TJ_ERR_ALIGN;
+  const int64_t n4 = rows * (cols / 4);
+  hipLaunchKernelGGL(tj::bias_residual_kernel, dim3(tj::grid_for(n4)), dim3(tj::ET), 0, stream, out, x, y, bias, n4,
+                     cols / 4, seq_len, mode == 0 ? nullptr : valid_len, mode);
+  return tjh::launch_status();
+}
+
+extern "C" int tj_bias_gelu(float* y, const float* bias, int64_t rows, int64_t cols, hipStream_t stream) {
+  if (rows < 0 || cols <= 0) return TJ_ERR_SHAPE;
+  if (cols % 4 != 0) return TJ_ERR_UNSUPPORTED;
+  if (rows == 0) return TJ_OK;
+  if (!y || !bias) return TJ_ERR_SHAPE;
+  if (!tjh::aligned16(y) || !tjh::aligned16(bias)) return TJ_ERR_ALIGN;
+  const int64_t n4 = rows * (cols / 4);
+  hipLaunchKernelGGL(tj::bias_gelu_kernel, dim3(tj::grid_for(n4)), dim3(tj::ET), 0, stream, y, bias, n4, cols / 4);
+  return tjh::launch_status();
+}

@@ -156,12 +156,12 @@ class ExactOnlySelfAttention(StridedSDPASelfAttention):
         if valid_token_mask is not None:
             raise ValueError("trim padding before calling extreme attention")
 
-    def forward(self, x, valid_token_mask=None, causal=False, valid_len=None):
+    def context(self, x, valid_token_mask=None, causal=False, valid_len=None):
         self._check(x, valid_token_mask)
         b, s, _ = x.shape
         q, k, v = self.project_qkv(x)
         ctx = scaled_dot_product_attention(q, k, v, is_causal=causal, scale=self.scale)
-        return self.out_proj(ctx.transpose(1, 2).reshape(b, s, self.d_model))
+        return ctx.transpose(1, 2).reshape(b, s, self.d_model)
 
 
 class PolyOrExactSelfAttention(ExactOnlySelfAttention):
@@ -180,11 +180,11 @@ class PolyOrExactSelfAttention(ExactOnlySelfAttention):
     def route_name(self, sigma: Optional[float]) -> str:
         return "poly" if self.poly_enabled and poly_is_safe(sigma) else "exact"
 
-    def forward(self, x, valid_token_mask=None, causal=False, valid_len=None):
+    def context(self, x, valid_token_mask=None, causal=False, valid_len=None):
         self._check(x, valid_token_mask)
         if not causal:
             raise ValueError("the polynomial route is causal attention")
         b, s, _ = x.shape
         q, k, v = self.project_qkv(x)
         ctx, self.last_guard = guarded_attention(q, k, v, self.scale, enabled=self.poly_enabled)
-        return self.out_proj(ctx.transpose(1, 2).reshape(b, s, self.d_model))
+        return ctx.transpose(1, 2).reshape(b, s, self.d_model)

@@ -33,14 +33,11 @@ class StridedSDPASelfAttention(HipSelfAttention):
 
     drop_key_mask = False
 
-    def forward(self, x, valid_token_mask=None, causal=False, valid_len=None):
+    def context(self, x, valid_token_mask=None, causal=False, valid_len=None):
         b, s, _ = x.shape
         q, k, v = self.project_qkv(x)
         ctx = scaled_dot_product_attention(q, k, v, is_causal=causal, scale=self.scale, valid_len=valid_len)
-        out = self.out_proj(ctx.transpose(1, 2).reshape(b, s, self.d_model))
-        if valid_token_mask is not None:
-            out = out.masked_fill(~valid_token_mask[..., None], 0)
-        return out
+        return ctx.transpose(1, 2).reshape(b, s, self.d_model)
 
 
 class PackedQKVSDPASelfAttention(StridedSDPASelfAttention):

@@ -1,0 +1,56 @@
+"""Fused elementwise tails of the encoder block on the HIP kernels.
+
+``bias_residual`` and ``bias_gelu`` replace the bias add / residual add /
+``masked_fill`` and bias add / exact GELU pairs that follow the block's
+projection GEMMs (``torch_transformer_benchmark.py:116-121``, ``:140-145``)
+with one pass each. Both return ``None`` for layouts the kernels do not take
+(non-fp32, a last dimension that is not a multiple of 4, unaligned or
+non-contiguous tensors), and the caller then uses the plain tensor ops.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+from .attention import _stream_ptr
+
+MODE_PLAIN = 0       # out = x + y + b
+MODE_ZERO_Y = 1      # out = x + (row valid ? y + b : 0)
+MODE_ZERO_OUT = 2    # out = row valid ? x + y + b : 0
+
+
+def _ok(*ts: torch.Tensor) -> bool:
+    return all(t.is_cuda and t.dtype == torch.float32 and t.is_contiguous() and t.data_ptr() % 16 == 0
+               and t.shape[-1] % 4 == 0 for t in ts)
+
+
+def bias_residual(x: torch.Tensor, y: torch.Tensor, bias: torch.Tensor, valid_len: Optional[torch.Tensor],
+                  mode: int, out: Optional[torch.Tensor] = None) -> Optional[torch.Tensor]:
+    """One pass of ``x + y + bias`` with padded rows handled per ``mode``; ``x``, ``y`` ``[B, S, C]``."""
+    if x.ndim != 3 or y.shape != x.shape or bias.shape != (x.shape[-1],):
+        return None
+    if valid_len is not None and (valid_len.dtype != torch.int32 or valid_len.shape != (x.shape[0],)
+                                  or valid_len.device != x.device):
+        return None
+    out = torch.empty_like(x) if out is None else out
+    if not _ok(x, y, bias, out):
+        return None
+    b, s, c = x.shape
+    code = _lib.lib().tj_bias_residual(
+        out.data_ptr(), x.data_ptr(), y.data_ptr(), bias.data_ptr(), b * s, c, s,
+        None if valid_len is None else valid_len.data_ptr(), mode, _stream_ptr(x.device))
+    _lib.check(code, "tj_bias_residual")
+    return out
+
+
+def bias_gelu(y: torch.Tensor, bias: torch.Tensor) -> Optional[torch.Tensor]:
+    """``gelu(y + bias)`` (exact form) in place; ``y`` ``[..., C]``."""
+    if bias.ndim != 1 or y.shape[-1] != bias.shape[0] or not _ok(y, bias):
+        return None
+    code = _lib.lib().tj_bias_gelu(y.data_ptr(), bias.data_ptr(), y.numel() // y.shape[-1], y.shape[-1],
+                                   _stream_ptr(y.device))
+    _lib.check(code, "tj_bias_gelu")
+    return y

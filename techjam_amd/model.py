@@ -103,11 +103,15 @@ class HipSelfAttention(nn.Module):
     def attend(self, q, k, v, valid_len, causal):
         return scaled_dot_product_attention(q, k, v, is_causal=causal, scale=self.scale, valid_len=valid_len)
 
-    def forward(self, x, valid_token_mask=None, causal=False, valid_len=None):
+    def context(self, x, valid_token_mask=None, causal=False, valid_len=None):
+        """Attention output before the output projection, ``[B, S, D]`` (a free view)."""
         b, s, _ = x.shape
         q, k, v = self.project_qkv(x)
         ctx = self.attend(q, k, v, valid_len, causal)
-        out = self.out_proj(ctx.transpose(1, 2).reshape(b, s, self.d_model))
+        return ctx.transpose(1, 2).reshape(b, s, self.d_model)
+
+    def forward(self, x, valid_token_mask=None, causal=False, valid_len=None):
+        out = self.out_proj(self.context(x, valid_token_mask, causal, valid_len))
         if valid_token_mask is not None:
             out = out.masked_fill(~valid_token_mask[..., None], 0)
         return out
@@ -125,11 +129,41 @@ class EncoderBlock(nn.Module):
         self.ffn_out = Linear(ffn_dim, d_model)
 
     def forward(self, x, valid_token_mask, causal, valid_len=None):
+        if self._can_fuse(x, valid_token_mask, valid_len):
+            return self._forward_fused(x, valid_token_mask, causal, valid_len)
         x = x + self.attention(self.norm1(x), valid_token_mask, causal, valid_len=valid_len)
         x = x + self.ffn_out(F.gelu(self.ffn_in(self.norm2(x)), approximate="none"))
         if valid_token_mask is not None:
             x = x.masked_fill(~valid_token_mask[..., None], 0)
         return x
+
+    def _can_fuse(self, x, valid_token_mask, valid_len) -> bool:
+        return (x.is_cuda and x.dtype == torch.float32 and x.ndim == 3 and x.is_contiguous()
+                and x.data_ptr() % 16 == 0 and x.shape[-1] % 4 == 0 and self.ffn_in.out_features % 4 == 0
+                and (valid_token_mask is None or valid_len is not None)
+                and self.attention.out_proj.bias is not None and self.ffn_in.bias is not None
+                and self.ffn_out.bias is not None)
+
+    def _forward_fused(self, x, valid_token_mask, causal, valid_len):
+        """Same computation as the unfused forward; the projection GEMMs run
+        bias-free and each bias add, residual add, GELU and row zeroing is
+        folded into one pass over the GEMM output."""
+        from .kernels.elementwise import MODE_ZERO_OUT, MODE_ZERO_Y, bias_gelu, bias_residual
+
+        attn = self.attention
+        ctx = attn.context(self.norm1(x), valid_token_mask, causal, valid_len)
+        y = F.linear(ctx, attn.out_proj.weight)
+        x = _must(bias_residual(x, y, attn.out_proj.bias, valid_len, MODE_ZERO_Y, out=y))
+        h = F.linear(self.norm2(x), self.ffn_in.weight)
+        _must(bias_gelu(h, self.ffn_in.bias))
+        y = F.linear(h, self.ffn_out.weight)
+        return _must(bias_residual(x, y, self.ffn_out.bias, valid_len, MODE_ZERO_OUT, out=y))
+
+
+def _must(t):
+    if t is None:
+        raise RuntimeError("the fused block kernels rejected a layout the block checked beforehand")
+    return t
 
 
 class TransformerEncoder(nn.Module):

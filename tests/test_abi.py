@@ -178,3 +178,17 @@ def test_poly_parts_refuse_cpu_tensors():
         quad_update(a, a, torch.zeros(2, 4096, 64))
     with pytest.raises(UnsupportedCaseError):
         causal_diag(a, a, a)
+
+
+def test_block_tails_reject_bad_arguments_before_launching():
+    from techjam_amd.kernels import _lib
+
+    L = _lib.lib()
+    assert L.tj_bias_residual(16, 16, 16, 16, 4, 6, 2, None, 0, None) == _lib.TJ_ERR_UNSUPPORTED
+    assert L.tj_bias_residual(16, 16, 16, 16, 4, 8, 2, None, 3, None) == _lib.TJ_ERR_SHAPE
+    assert L.tj_bias_residual(16, 16, 16, 16, 5, 8, 2, 16, 1, None) == _lib.TJ_ERR_SHAPE
+    assert L.tj_bias_residual(16, 24, 16, 16, 4, 8, 2, None, 0, None) == _lib.TJ_ERR_ALIGN
+    assert L.tj_bias_residual(16, 16, 16, 16, 0, 8, 2, None, 0, None) == _lib.TJ_OK
+    assert L.tj_bias_gelu(16, 16, 4, 6, None) == _lib.TJ_ERR_UNSUPPORTED
+    assert L.tj_bias_gelu(8, 16, 4, 8, None) == _lib.TJ_ERR_ALIGN
+    assert L.tj_bias_gelu(16, 16, -1, 8, None) == _lib.TJ_ERR_SHAPE

@@ -1,0 +1,73 @@
+"""Fused block tails (bias + residual + row zeroing, bias + exact GELU) against
+the plain tensor ops they replace (GPU)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(cuda, b=3, s=37, c=64, seed=0):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    x = torch.randn(b, s, c, generator=g, device="cuda")
+    y = torch.randn(b, s, c, generator=g, device="cuda")
+    bias = torch.randn(c, generator=g, device="cuda")
+    lens = torch.tensor([s, 1, s // 2][:b], dtype=torch.int32, device="cuda")
+    mask = torch.arange(s, device="cuda")[None, :] < lens[:, None]
+    return x, y, bias, lens, mask
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_bias_residual_modes_match_tensor_ops(cuda, masked):
+    from techjam_amd.kernels.elementwise import MODE_PLAIN, MODE_ZERO_OUT, MODE_ZERO_Y, bias_residual
+
+    x, y, bias, lens, mask = _case(cuda)
+    vl = lens if masked else None
+    m = mask[..., None] if masked else torch.ones_like(mask)[..., None]
+    want0 = x + (y + bias)
+    want1 = x + (y + bias).masked_fill(~m, 0)
+    want2 = (x + (y + bias)).masked_fill(~m, 0)
+    assert torch.equal(bias_residual(x, y, bias, None, MODE_PLAIN), want0)
+    assert torch.equal(bias_residual(x, y, bias, vl, MODE_ZERO_Y), want1)
+    assert torch.equal(bias_residual(x, y, bias, vl, MODE_ZERO_OUT), want2)
+
+
+def test_bias_residual_may_write_over_its_input(cuda):
+    from techjam_amd.kernels.elementwise import MODE_ZERO_OUT, bias_residual
+
+    x, y, bias, lens, mask = _case(cuda, seed=1)
+    want = (x + (y + bias)).masked_fill(~mask[..., None], 0)
+    out = bias_residual(x, y, bias, lens, MODE_ZERO_OUT, out=y)
+    assert out.data_ptr() == y.data_ptr() and torch.equal(out, want)
+
+
+def test_bias_residual_zeroes_non_finite_padded_rows(cuda):
+    from techjam_amd.kernels.elementwise import MODE_ZERO_OUT, MODE_ZERO_Y, bias_residual
+
+    x, y, bias, lens, mask = _case(cuda, seed=2)
+    y[1, 5:] = float("inf")  # padded rows of sample 1 (length 1)
+    assert torch.isfinite(bias_residual(x, y, bias, lens, MODE_ZERO_Y)).all()
+    out = bias_residual(x, y, bias, lens, MODE_ZERO_OUT)
+    assert float(out[~mask].abs().max()) == 0.0
+
+
+def test_bias_gelu_matches_exact_gelu(cuda):
+    from techjam_amd.kernels.elementwise import bias_gelu
+
+    x, y, bias, _, _ = _case(cuda, c=256, seed=3)
+    want = F.gelu(y * 3 + bias, approximate="none")
+    got = bias_gelu((y * 3).contiguous(), bias)
+    assert (got - want).abs().max().item() < 1e-6
+
+
+def test_unsupported_layouts_are_declined(cuda):
+    from techjam_amd.kernels.elementwise import MODE_PLAIN, bias_gelu, bias_residual
+
+    x, y, bias, _, _ = _case(cuda, c=66)
+    assert bias_residual(x, y, bias, None, MODE_PLAIN) is None        # width not a multiple of 4
+    x, y, bias, _, _ = _case(cuda)
+    assert bias_residual(x.transpose(0, 1), y.transpose(0, 1), bias, None, MODE_PLAIN) is None
+    assert bias_gelu(y.half(), bias.half()) is None                     # fp32 only
