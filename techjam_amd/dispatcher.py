@@ -75,7 +75,7 @@ OFFICIAL_CASE_BY_CONFIG: Dict[ConfigKey, int] = {
 BENCHMARK_CASE_BY_CONFIG: Dict[ConfigKey, str] = {
     cfg.model_key(): name for name, cfg in BENCHMARK_CONFIGS.items() if cfg.model_key() is not None
 }
-PACKED_QKV_CASES = frozenset((2, 3, "C2"))
+PACKED_QKV_CASES = frozenset((2, 3, "C2", "C4"))
 EXTREME_CASES = (6, 14)
 
 

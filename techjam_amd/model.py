@@ -183,7 +183,7 @@ class TransformerEncoder(nn.Module):
             x = layer(x, valid_token_mask, self.config.causal, valid_len=valid_len)
         x = self.final_norm(x)
         if valid_token_mask is not None:
-            x = x.masked_fill(~valid_token_mask[..., None], 0)
+            x.masked_fill_(~valid_token_mask[..., None], 0)  # x is the norm's fresh output
         return x
 
     def forward(self, x, valid_token_mask: Optional[torch.Tensor] = None):
