@@ -42,7 +42,7 @@ constexpr int PD = 64;         // head dim (d = dv)
 constexpr int PC = 512;        // chunk length
 constexpr int PT = 256;        // threads per workgroup
 constexpr int NAPPLY = 4;      // apply workgroups per head and chunk (128 rows each)
-constexpr int NUPD = 8;        // quad-update workgroups per head (8 i-slices each)
+constexpr int NUPD = 6;        // quad-update workgroups per head (4 for i < 32, 2 for i >= 32)
 constexpr int KG = 4;          // chunks per launch (update sub-chunks, apply groups)
 constexpr int NSLOT = 2 * KG;  // shadow slots: state_c lives in slot c % NSLOT
 constexpr int NROLE = KG * NAPPLY + NUPD + 1;
@@ -500,68 +500,72 @@ __device__ __forceinline__ void update_range(const PolyArgs& a, int& c0, int& c1
   c1 = min(c0 + KG, a.n_chunks - 1);
 }
 
-template <typename T>
-__device__ void quad_update_role(const PolyArgs& a, char* ws, int b, int h, int ug, char* smem) {
+// NI i-slices per wave, j-blocks JB0..1 (the apply never reads j < 32 for
+// i >= 32: S is symmetric).
+template <typename T, int NI, int JB0>
+__device__ void quad_update_body(const PolyArgs& a, char* ws, int b, int h, int i0, char* smem) {
   int c0, c1;
   update_range(a, c0, c1);
   if (c0 >= c1) return;
-  const int w = threadIdx.x / kWave, lane = threadIdx.x % kWave, hl = lane / 32, ln = lane % 32;
-  const int i0 = 8 * ug + 2 * w;  // this wave's two i-slices
+  constexpr int NJ = 2 - JB0;
+  const int lane = threadIdx.x % kWave, hl = lane / 32, ln = lane % 32;
   float* img = reinterpret_cast<float*>(ws + kQuadImg);
-  // acc[ii][jb][vb] = D[j][v] block of S_i (rows j, columns v). The fp32
+  // acc[ii][jj][vb] = D[j][v] block (jb = JB0 + jj) of S_{i0+ii}. The fp32
   // master stays in these registers across the launch's chunks.
-  float16_t acc[2][2][2];
-  // The apply reads S_ij only for j at or above i's 16-block (S is
-  // symmetric): for i >= 32 the block j < 32 is neither formed nor stored.
-  const int jb0 = i0 >= 32 ? 1 : 0;
+  float16_t acc[NI][NJ][2];
 #pragma unroll
-  for (int ii = 0; ii < 2; ++ii)
+  for (int ii = 0; ii < NI; ++ii)
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb)
+    for (int jj = 0; jj < NJ; ++jj)
 #pragma unroll
-      for (int vb = 0; vb < 2; ++vb)
-        if (jb >= jb0) load_img(img + ((size_t(i0 + ii) * 2 + jb) * 2 + vb) * 1024, acc[ii][jb][vb]);
+      for (int vb = 0; vb < 2; ++vb) load_img(img + ((size_t(i0 + ii) * 2 + JB0 + jj) * 2 + vb) * 1024, acc[ii][jj][vb]);
 
   for (int c = c0; c < c1; ++c) {
     stream_tokens<T>(a, b, h, c * PC, min(a.S, c * PC + PC), smem, [&](half_t (*bt)[LP], half_t (*vt)[LP], int tk) {
       const int t = tk + 8 * hl;
-      half8_t bj[2], vv[2];
+      half8_t bj[NJ], vv[2];
 #pragma unroll
-      for (int x = 0; x < 2; ++x) {
-        if (x >= jb0) bj[x] = *reinterpret_cast<const half8_t*>(&bt[32 * x + ln][t]);
-        vv[x] = *reinterpret_cast<const half8_t*>(&vt[32 * x + ln][t]);
-      }
+      for (int jj = 0; jj < NJ; ++jj) bj[jj] = *reinterpret_cast<const half8_t*>(&bt[32 * (JB0 + jj) + ln][t]);
 #pragma unroll
-      for (int ii = 0; ii < 2; ++ii) {
+      for (int x = 0; x < 2; ++x) vv[x] = *reinterpret_cast<const half8_t*>(&vt[32 * x + ln][t]);
+#pragma unroll
+      for (int ii = 0; ii < NI; ++ii) {
         const half8_t bi = *reinterpret_cast<const half8_t*>(&bt[i0 + ii][t]);
 #pragma unroll
-        for (int jb = 0; jb < 2; ++jb) {
-          if (jb < jb0) continue;
+        for (int jj = 0; jj < NJ; ++jj) {
           half8_t phi;
 #pragma unroll
-          for (int j = 0; j < 8; ++j) phi[j] = bj[jb][j] * bi[j];
+          for (int j = 0; j < 8; ++j) phi[j] = bj[jj][j] * bi[j];
 #pragma unroll
-          for (int vb = 0; vb < 2; ++vb) acc[ii][jb][vb] = mfma32(phi, vv[vb], acc[ii][jb][vb]);
+          for (int vb = 0; vb < 2; ++vb) acc[ii][jj][vb] = mfma32(phi, vv[vb], acc[ii][jj][vb]);
         }
       }
     });
     // fp16 shadow of state_{c+1} for the applies of the next launch.
     half_t* sh = reinterpret_cast<half_t*>(ws + kQuadShadow) + size_t((c + 1) % NSLOT) * PD * PD * PD;
 #pragma unroll
-    for (int ii = 0; ii < 2; ++ii)
+    for (int ii = 0; ii < NI; ++ii)
 #pragma unroll
-      for (int jb = 0; jb < 2; ++jb)
+      for (int jj = 0; jj < NJ; ++jj)
 #pragma unroll
-        for (int vb = 0; vb < 2; ++vb)
-          if (jb >= jb0) store_shadow_t(sh + size_t(i0 + ii) * PD * PD, acc[ii][jb][vb], jb, vb);
+        for (int vb = 0; vb < 2; ++vb) store_shadow_t(sh + size_t(i0 + ii) * PD * PD, acc[ii][jj][vb], JB0 + jj, vb);
   }
 #pragma unroll
-  for (int ii = 0; ii < 2; ++ii)
+  for (int ii = 0; ii < NI; ++ii)
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb)
+    for (int jj = 0; jj < NJ; ++jj)
 #pragma unroll
-      for (int vb = 0; vb < 2; ++vb)
-        if (jb >= jb0) store_img(img + ((size_t(i0 + ii) * 2 + jb) * 2 + vb) * 1024, acc[ii][jb][vb]);
+      for (int vb = 0; vb < 2; ++vb) store_img(img + ((size_t(i0 + ii) * 2 + JB0 + jj) * 2 + vb) * 1024, acc[ii][jj][vb]);
+}
+
+// Quad-update workgroups 0..3: i < 32, two slices per wave, both j-blocks;
+// workgroups 4..5: i >= 32, four slices per wave, j >= 32 only -- the same
+// MFMA count per wave.
+template <typename T>
+__device__ void quad_update_role(const PolyArgs& a, char* ws, int b, int h, int ug, char* smem) {
+  const int w = threadIdx.x / kWave;
+  if (ug < 4) quad_update_body<T, 2, 0>(a, ws, b, h, 8 * ug + 2 * w, smem);
+  else quad_update_body<T, 4, 1>(a, ws, b, h, 32 + 16 * (ug - 4) + 4 * w, smem);
 }
 
 template <typename T>
