@@ -46,7 +46,8 @@ def parse_args():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--workload", default="attn-core",
-                   choices=["attn-core", "extreme", "model-c1", "model-c2", "model-c4", "copy-1gib"])
+                   choices=["attn-core", "extreme", "model-c1", "model-c2", "model-c4", "copy-1gib",
+                            "quad-apply", "quad-update", "causal-diag"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-repeats", type=int, default=3)
     # Float32 GEMM flags of the model workloads; the defaults are the reference
@@ -57,11 +58,17 @@ def parse_args():
 
 
 def traffic_from_profiles(name: str):
-    """HBM bytes per launch recorded by the rocprofv3 counter runs, if committed."""
+    """HBM bytes per launch recorded by the rocprofv3 counter runs, if committed.
+
+    `name` is a file under profiles/, optionally `file#kernel` for a summary
+    that records several kernels (`traffic_bytes_per_launch[kernel]: ...`).
+    """
+    name, _, kernel = name.partition("#")
     path = ROOT / "profiles" / name
     if not path.exists():
         return None
-    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", path.read_text(), re.M)
+    key = r"traffic_bytes_per_launch" + (r"\[" + re.escape(kernel) + r"\]" if kernel else "")
+    m = re.search(r"^" + key + r":\s*([0-9.eE+]+)", path.read_text(), re.M)
     return float(m.group(1)) if m else None
 
 
@@ -99,6 +106,41 @@ def copy_1gib(args, dev):
 
     config = {"workload": "calibration: torch device copy of 2^28 fp32 (1 GiB read + 1 GiB write)"}
     return step, n, 0.0, 2.0 * 4 * n, config, "copy_1gib_calibration.md"
+
+
+def poly_part(name):
+    """One stand-alone polynomial kernel at the reference's quoted shape
+    (M=32 (b, h) pairs, C=512 tokens, D=V=64, the shape its timings for
+    src/kernels/poly_attention_triton.py are quoted at)."""
+    def build(args, dev):
+        from techjam_amd.kernels.poly_parts import causal_diag, quad_apply, quad_update
+
+        m, c, d = 32, 512, 64
+        kernel = name.replace("-", "_")
+        g = torch.Generator(device=dev).manual_seed(1234 + 100000)
+        a, b, v = (torch.randn(m, c, d, generator=g, device=dev, dtype=torch.float16) * 0.2 for _ in range(3))
+        state = torch.randn(m, d * d, d, generator=g, device=dev)
+        shadow = torch.zeros(m, d * d, d, device=dev, dtype=torch.float16)
+        if name == "quad-apply":
+            def step():
+                quad_apply(a, state)
+            flops, nbytes = 2.0 * m * c * d ** 3, m * d ** 3 * 4 + 2 * m * c * d * 2
+        elif name == "quad-update":
+            def step():
+                quad_update(b, v, state, shadow=shadow)
+            flops, nbytes = 2.0 * m * c * d ** 3, 2 * m * d ** 3 * 4 + m * d ** 3 * 2 + 2 * m * c * d * 2
+        else:
+            def step():
+                causal_diag(a, b, v)
+            flops, nbytes = 2.0 * m * d * c * (c + 1), 3 * m * c * d * 2 + m * c * (d + 1) * 4
+        config = {"workload": f"stand-alone {kernel}: M={m} (b, h) pairs, C={c} tokens, D=V={d}, "
+                              "fp16 operands, fp32 state", "m": m, "chunk": c, "head_dim": d,
+                  # the update reads and writes the fp32 state once per call: HBM sets its floor
+                  "bound": "hbm" if name == "quad-update" else "mfma",
+                  "data": "synthetic: a, b, v ~ N(0, 0.2^2) fp16, state ~ N(0, 1) fp32, generated on the GPU "
+                          "(seed 101234)"}
+        return step, m * c, flops, float(nbytes), config, "poly_parts_m32_c512_d64.md#" + kernel
+    return build
 
 
 def extreme(args, dev):
@@ -209,6 +251,8 @@ def main():
     torch.backends.cuda.matmul.allow_tf32 = False
 
     builders = {"attn-core": attn_core, "extreme": extreme, "copy-1gib": copy_1gib,
+                "quad-apply": poly_part("quad-apply"), "quad-update": poly_part("quad-update"),
+                "causal-diag": poly_part("causal-diag"),
                 "model-c1": model("C1"), "model-c2": model("C2"), "model-c4": model("C4")}
     step, tokens, flops, bytes_alg, config, prof_name = builders[args.workload](args, dev)
     if args.workload != "attn-core":
@@ -234,13 +278,14 @@ def main():
     sec = ms_per_step / 1e3
     tflops = flops / sec / 1e12
     hbm_gbs = bytes_alg / sec / 1e9
+    bound = config.pop("bound", "mfma" if flops else "hbm")
     roofline = {
         "bound": "mfma",
         "achieved": round(tflops, 2),
         "peak": PEAK_MFMA_F16_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(tflops / PEAK_MFMA_F16_TFLOPS, 4),
-    } if flops else {
+    } if bound == "mfma" else {
         "bound": "hbm",
         "achieved": round(hbm_gbs, 1),
         "peak": PEAK_HBM_GBS,
@@ -268,7 +313,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16",
-        "data": "synthetic: q, k, v ~ N(0, 1) generated on the GPU (seed 101234)",
+        "data": config.pop("data", "synthetic: q, k, v ~ N(0, 1) generated on the GPU (seed 101234)"),
         "config": config,
         "roofline": roofline,
         "cpu_baseline": cpu,

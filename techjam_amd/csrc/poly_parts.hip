@@ -136,11 +136,32 @@ struct StateSlice {
   }
 };
 
+// The row blocks of one m read the same 1 MiB state: the linear block id is
+// remapped so that they run on one XCD (ids are dealt round-robin over the
+// XCDs) and share its L2. Returns false for padding ids.
+__device__ __forceinline__ bool xcd_block(int n_rb, int M, int& m, int& rb) {
+  const int total = n_rb * M;
+  const int per_xcd = (total + kNumXcd - 1) / kNumXcd;
+  const int id = blockIdx.x;
+  const int logical = (id % kNumXcd) * per_xcd + id / kNumXcd;
+  if (logical >= total) return false;
+  m = logical / n_rb;
+  rb = logical % n_rb;
+  return true;
+}
+
+unsigned xcd_grid(int n_rb, int64_t M) {
+  const int64_t total = n_rb * M;
+  return (unsigned)(((total + kNumXcd - 1) / kNumXcd) * kNumXcd);
+}
+
 template <typename TS>
 __global__ __launch_bounds__(XT, 2) void quad_apply_kernel(ApplyArgs a) {
   __shared__ half_t sst[2][XD][XLP];
   __shared__ half_t at[128][XAP];
-  const int m = blockIdx.y, c0 = 128 * blockIdx.x;
+  int m, rb;
+  if (!xcd_block((a.C + 127) / 128, a.M, m, rb)) return;
+  const int c0 = 128 * rb;
   const int tid = threadIdx.x, w = tid / kWave, lane = tid % kWave, hl = lane / 32, ln = lane % 32;
   half8_t aB[4];
   load_a_rows(a.a, a.va, m, c0, a.C, aB, at);
@@ -197,6 +218,10 @@ struct UpdateArgs {
 };
 
 // One workgroup per (m, 4 consecutive i); wave w owns i = 4 blockIdx.x + w.
+// Consecutive workgroups land on different XCDs: each XCD then re-reads b and
+// v of the head from HBM (2x the algorithmic fetch), but the state traffic
+// spreads more evenly and the launch runs ~5 % faster than with the 16
+// workgroups of one m kept on one XCD.
 // acc[jb][vb] holds D[j][v] of S_i, i.e. state rows i*64 + j, columns v.
 __global__ __launch_bounds__(XT, 2) void quad_update_kernel(UpdateArgs a) {
   __shared__ half_t bt[2][XD][XLP];
@@ -385,7 +410,7 @@ extern "C" int tj_quad_apply(const void* a, const void* s, void* y, int s_dtype,
   if (M < 0 || C < 0 || D <= 0 || V <= 0) return TJ_ERR_SHAPE;
   if (D != tj::XD || V != tj::XD) return TJ_ERR_UNSUPPORTED;
   if (M == 0 || C == 0) return TJ_OK;
-  if (M >= 65536 || C >= (int64_t(1) << 30)) return TJ_ERR_SHAPE;
+  if (M >= 65536 || C >= (int64_t(1) << 30) || ((C + 127) / 128) * M >= (int64_t(1) << 31)) return TJ_ERR_SHAPE;
   if (!tj::view3_ok(a, a_strides, 2) || !tj::view3_ok(s, s_strides, tjh::elem_size(s_dtype)) ||
       !tj::view3_ok(y, y_strides, 2))
     return TJ_ERR_ALIGN;
@@ -398,7 +423,7 @@ extern "C" int tj_quad_apply(const void* a, const void* s, void* y, int s_dtype,
   args.vy = {y_strides[0], y_strides[1]};
   args.M = (int)M;
   args.C = (int)C;
-  const dim3 grid((unsigned)((C + 127) / 128), (unsigned)M);
+  const dim3 grid(tj::xcd_grid((int)((C + 127) / 128), M));
   if (s_dtype == TJ_F32) hipLaunchKernelGGL(tj::quad_apply_kernel<float>, grid, dim3(tj::XT), 0, stream, args);
   else hipLaunchKernelGGL(tj::quad_apply_kernel<half_t>, grid, dim3(tj::XT), 0, stream, args);
   return tjh::launch_status();
