@@ -11,8 +11,8 @@
 //   S_quad[(i,j), v] += sum_t b_ti b_tj v_tv,  S_lin[j, v] += sum_t b_tj v_tv,
 //   G[i, j] += sum_t b_ti b_tj,  z[j] += sum_t b_tj,  S_const[v] += sum_t v_tv.
 //
-// Launches advance four chunks at a time; in launch L every head owns 25
-// workgroups with three roles:
+// Launches advance four chunks at a time; in launch L every head owns 27
+// workgroups with four roles:
 //   * apply (4 per chunk, 128 rows each, for the four chunks whose start
 //     states the previous launch produced): quadratic term as
 //       y^T = sum_i S_i^T (a_i * a^T)  (S_i = rows (i, .) of S_quad),
@@ -20,13 +20,17 @@
 //     registers -- phi2(a) never exists in memory; linear and denominator terms
 //     as three more small GEMMs; the exact diagonal block like the exact
 //     kernel (S^T = b a^T in registers, no max subtraction).
-//   * quad update (8 per head, 8 i-slices each): S_i += (b_i * b)^T v over the
-//     tokens of chunks [4L, 4L + 4), accumulated straight into MFMA
-//     accumulators that hold the fp32 master in its register image (the
-//     master's memory layout IS the accumulator layout, so loading and storing
-//     it is straight 16-byte copies, once per launch). After each chunk it
-//     writes the fp16 shadow of the state the apply of the next chunk reads.
+//   * quad update (6 per head): S_i += (b_i * b)^T v over the tokens of
+//     chunks [4L, 4L + 4), accumulated straight into MFMA accumulators that
+//     hold the fp32 master in its register image (the master's memory layout
+//     IS the accumulator layout, so loading and storing it is straight 16-byte
+//     copies, once per launch). After each chunk it writes the fp16 shadow of
+//     the state the apply of the next chunk reads.
 //   * small-state update (1 per head): S_lin, G, z, S_const, likewise.
+//   * token images (4 per head): b = k*sqrt(scale) and v of the chunks the
+//     next launch folds in, converted once to fp16 tiles laid out as the
+//     update roles' LDS image, which those roles then stream with direct
+//     global->LDS copies.
 // State c (before chunk c) lives in shadow slot c % 8: a launch reads the
 // slots of states 4L-3 .. 4L and writes those of 4L+1 .. 4L+4, so applies and
 // updates of one launch never touch the same slot.
@@ -45,7 +49,8 @@ constexpr int NAPPLY = 4;      // apply workgroups per head and chunk (128 rows 
 constexpr int NUPD = 6;        // quad-update workgroups per head (4 for i < 32, 2 for i >= 32)
 constexpr int KG = 4;          // chunks per launch (update sub-chunks, apply groups)
 constexpr int NSLOT = 2 * KG;  // shadow slots: state_c lives in slot c % NSLOT
-constexpr int NROLE = KG * NAPPLY + NUPD + 1;
+constexpr int NCONV = KG;      // token-image workgroups per head (one chunk each)
+constexpr int NROLE = KG * NAPPLY + NUPD + 1 + NCONV;
 constexpr int LP = 72;         // padded LDS row of 64 halves (144 bytes)
 constexpr int kBufferFlags = 0x00020000;  // raw (untyped) buffer resource word 3 on gfx950
 constexpr int AP = 66;         // padded LDS row of the a tile (132 bytes, conflict-free u16 reads)
@@ -60,7 +65,12 @@ constexpr size_t kQuadShadow = kZsMaster + 128 * 4;              // fp16 [NSLOT]
 constexpr size_t kLinShadow = kQuadShadow + NSLOT * size_t(PD) * PD * PD * 2;  // fp16 [NSLOT][64 v][64 j]
 constexpr size_t kGramShadow = kLinShadow + NSLOT * PD * PD * 2;  // fp16 [NSLOT][64][64] (symmetric)
 constexpr size_t kZsShadow = kGramShadow + NSLOT * PD * PD * 2;   // fp32 [NSLOT][128]
-constexpr size_t kPerHead = (kZsShadow + NSLOT * 128 * 4 + 255) & ~size_t(255);
+// Token images: the k (scaled) and v tiles the update roles of a launch fold
+// in, written once by the previous launch as fp16 LDS images (see TokTile).
+constexpr int kTileImg = 2 * PD * 64 * 2;                          // [b^T | v^T] of 64 tokens
+constexpr size_t kTokImgBytes = size_t(KG) * (PC / 64) * kTileImg;  // one launch: 512 KiB
+constexpr size_t kTokImg = (kZsShadow + NSLOT * 128 * 4 + 255) & ~size_t(255);  // [2][kTokImgBytes]
+constexpr size_t kPerHead = kTokImg + 2 * kTokImgBytes;
 
 // LDS: apply = quad-state ring (49152) or diagonal tiles (36864), + a tile (16896);
 //      updates = two transposed token tiles, double buffered (36864).
@@ -85,8 +95,7 @@ struct PolyArgs {
   const float* coeffs;  // [M][3]
   const int32_t* flags; // [M] or null
   char* ws;
-  int total;            // M * NROLE
-  int per_xcd;
+  int M;                // B * H
 };
 
 __device__ __forceinline__ float4_t ld4(const float* p) { return *reinterpret_cast<const float4_t*>(p); }
@@ -147,16 +156,21 @@ struct TokTile {
       }
     }
   }
-  // Both transposed ([dim][token], token order as given): the update roles.
-  __device__ __forceinline__ void store_transposed(half_t (*bt)[LP], half_t (*vt)[LP], float rs, int tid) const {
+  // The tile's LDS image for the update roles, stored to global memory:
+  // [b^T | v^T], each 64 dim rows of 128 bytes (64 tokens), the eight
+  // 16-byte pieces of row d at position piece ^ ((d >> 1) & 7) so that 16
+  // lanes reading one piece column of 16 consecutive rows hit distinct banks.
+  __device__ __forceinline__ void store_image(char* dst, float rs, int tid) const {
     int g, c;
     coords(tid, g, c);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      half4_t hb = {(half_t)(kx[0][e] * rs), (half_t)(kx[1][e] * rs), (half_t)(kx[2][e] * rs), (half_t)(kx[3][e] * rs)};
-      half4_t hv = {(half_t)vx[0][e], (half_t)vx[1][e], (half_t)vx[2][e], (half_t)vx[3][e]};
-      *reinterpret_cast<half4_t*>(&bt[4 * c + e][4 * g]) = hb;
-      *reinterpret_cast<half4_t*>(&vt[4 * c + e][4 * g]) = hv;
+      const int d = 4 * c + e;
+      const int off = d * 128 + 16 * ((g >> 1) ^ ((d >> 1) & 7)) + 8 * (g & 1);
+      *reinterpret_cast<half4_t*>(dst + off) =
+          half4_t{(half_t)(kx[0][e] * rs), (half_t)(kx[1][e] * rs), (half_t)(kx[2][e] * rs), (half_t)(kx[3][e] * rs)};
+      *reinterpret_cast<half4_t*>(dst + PD * 128 + off) =
+          half4_t{(half_t)vx[0][e], (half_t)vx[1][e], (half_t)vx[2][e], (half_t)vx[3][e]};
     }
   }
   // K row-major, V transposed in key_slot order: the diagonal block (as in the exact kernel).
@@ -441,26 +455,73 @@ __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int 
 // Update roles: fold the chunk's tokens into the states.
 // ---------------------------------------------------------------------------
 
-// Streams the chunk's tokens through LDS as transposed fp16 tiles and calls
-// body(bt, vt, tok) for every 16-token MFMA k-step.
-template <typename T, typename Body>
-__device__ __forceinline__ void stream_tokens(const PolyArgs& a, int b, int h, int t0, int t1, char* smem, Body&& body) {
-  auto bt = reinterpret_cast<half_t(*)[64][LP]>(smem);
-  auto vt = reinterpret_cast<half_t(*)[64][LP]>(smem + 2 * 64 * LP * 2);
-  const int tid = threadIdx.x;
-  const int n_blk = (t1 - t0 + 63) / 64;
-  TokTile<T> tile;
-  tile.init(a, b, h, tid);
-  tile.load(t0);
-  tile.store_transposed(bt[0], vt[0], a.rs, tid);
-  __syncthreads();
-  for (int blk = 0; blk < n_blk; ++blk) {
-    const int cur = blk & 1;
-    if (blk + 1 < n_blk) tile.load(t0 + 64 * (blk + 1));
+// The token images of the chunks this launch folds in stream through a ring
+// of three LDS stages by direct global->LDS copies issued two tiles ahead (no
+// registers held). body(bT, vT) runs on every 64-token tile (b^T and v^T, 64
+// dim rows of 128 bytes with XOR-placed 16-byte pieces, see img_piece);
+// chunk_end(j) after the last tile of the launch's j-th chunk. The stages are
+// distinct members addressed with compile-time indices, so the compiler can
+// tell the copies into one stage from the reads of another.
+struct TokRing {
+  char s0[kTileImg];
+  char s1[kTileImg];
+  char s2[kTileImg];
+};
+static_assert(sizeof(TokRing) <= kStageBytes, "the token ring must fit the ring area");
+
+// Tokens 8 pc .. 8 pc + 7 of dim row `row` of a tile image.
+__device__ __forceinline__ half8_t img_piece(const half_t* base, int row, int pc) {
+  return *reinterpret_cast<const half8_t*>(reinterpret_cast<const char*>(base) + row * 128 + 16 * (pc ^ ((row >> 1) & 7)));
+}
+
+template <typename Body, typename ChunkEnd>
+__device__ __forceinline__ void stream_image(const char* img, int n_chunk, char* smem, Body&& body,
+                                             ChunkEnd&& chunk_end) {
+  constexpr int kTiles = PC / 64;
+  TokRing& ring = *reinterpret_cast<TokRing*>(smem);
+  const int w = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int n = n_chunk * kTiles;
+  auto stage_ptr = [&](auto st) -> char* {
+    if constexpr (decltype(st)::value == 0) return ring.s0;
+    else if constexpr (decltype(st)::value == 1) return ring.s1;
+    else return ring.s2;
+  };
+  // Copy instruction `it` of wave w moves 1 KiB slot 4 it + w of the tile.
+  auto issue = [&](int t, auto st) {
+    char* base = stage_ptr(st);
+    const char* src = img + size_t(t) * kTileImg;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) body(bt[cur], vt[cur], 16 * ks);
-    if (blk + 1 < n_blk) tile.store_transposed(bt[cur ^ 1], vt[cur ^ 1], a.rs, tid);
-    __syncthreads();
+    for (int it = 0; it < 4; ++it) {
+      const int slot = 4 * it + w;
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(src + slot * 1024 + lane * 16),
+                                       (__attribute__((address_space(3))) void*)(base + slot * 1024), 16, 0, 0);
+    }
+  };
+  // Tile t + 1 (this wave's four copies) must have landed before the barrier;
+  // tile t + 2 may stay in flight (anything issued after it only makes the
+  // wait longer). A plain barrier: __syncthreads() would also wait for every
+  // copy in flight.
+  auto wait_next = [&](int t) {
+    if (t + 2 < n) __builtin_amdgcn_s_waitcnt(0x0074);  // vmcnt(4) lgkmcnt(0)
+    else __builtin_amdgcn_s_waitcnt(0x0070);            // vmcnt(0) lgkmcnt(0)
+    lds_barrier();
+  };
+  auto step = [&](int t, auto st) {
+    constexpr int sv = decltype(st)::value;
+    if (t + 2 < n) issue(t + 2, std::integral_constant<int, (sv + 2) % 3>{});
+    const char* base = stage_ptr(st);
+    body(reinterpret_cast<const half_t*>(base), reinterpret_cast<const half_t*>(base + PD * 128));
+    if ((t + 1) % kTiles == 0) chunk_end(t / kTiles);
+    wait_next(t);
+  };
+  if (n == 0) return;
+  issue(0, std::integral_constant<int, 0>{});
+  if (n > 1) issue(1, std::integral_constant<int, 1>{});
+  wait_next(-1);
+  for (int t = 0; t < n; t += 3) {
+    step(t, std::integral_constant<int, 0>{});
+    if (t + 1 < n) step(t + 1, std::integral_constant<int, 1>{});
+    if (t + 2 < n) step(t + 2, std::integral_constant<int, 2>{});
   }
 }
 
@@ -502,8 +563,8 @@ __device__ __forceinline__ void update_range(const PolyArgs& a, int& c0, int& c1
 
 // NI i-slices per wave, j-blocks JB0..1 (the apply never reads j < 32 for
 // i >= 32: S is symmetric).
-template <typename T, int NI, int JB0>
-__device__ void quad_update_body(const PolyArgs& a, char* ws, int b, int h, int i0, char* smem) {
+template <int NI, int JB0>
+__device__ __forceinline__ void quad_update_body(const PolyArgs& a, char* ws, int i0, char* smem) {
   int c0, c1;
   update_range(a, c0, c1);
   if (c0 >= c1) return;
@@ -520,36 +581,44 @@ __device__ void quad_update_body(const PolyArgs& a, char* ws, int b, int h, int 
 #pragma unroll
       for (int vb = 0; vb < 2; ++vb) load_img(img + ((size_t(i0 + ii) * 2 + JB0 + jj) * 2 + vb) * 1024, acc[ii][jj][vb]);
 
-  for (int c = c0; c < c1; ++c) {
-    stream_tokens<T>(a, b, h, c * PC, min(a.S, c * PC + PC), smem, [&](half_t (*bt)[LP], half_t (*vt)[LP], int tk) {
-      const int t = tk + 8 * hl;
-      half8_t bj[NJ], vv[2];
+  const char* tok = ws + kTokImg + size_t(a.launch & 1) * kTokImgBytes;
+  stream_image(
+      tok, c1 - c0, smem,
+      [&](const half_t* bT, const half_t* vT) {
 #pragma unroll
-      for (int jj = 0; jj < NJ; ++jj) bj[jj] = *reinterpret_cast<const half8_t*>(&bt[32 * (JB0 + jj) + ln][t]);
+        for (int ks = 0; ks < 4; ++ks) {
+          const int pc = 2 * ks + hl;  // tokens 16 ks + 8 hl .. +7 of the tile
+          half8_t bj[NJ], vv[2];
 #pragma unroll
-      for (int x = 0; x < 2; ++x) vv[x] = *reinterpret_cast<const half8_t*>(&vt[32 * x + ln][t]);
+          for (int jj = 0; jj < NJ; ++jj) bj[jj] = img_piece(bT, 32 * (JB0 + jj) + ln, pc);
 #pragma unroll
-      for (int ii = 0; ii < NI; ++ii) {
-        const half8_t bi = *reinterpret_cast<const half8_t*>(&bt[i0 + ii][t]);
+          for (int x = 0; x < 2; ++x) vv[x] = img_piece(vT, 32 * x + ln, pc);
 #pragma unroll
-        for (int jj = 0; jj < NJ; ++jj) {
-          half8_t phi;
+          for (int ii = 0; ii < NI; ++ii) {
+            const half8_t bi = img_piece(bT, i0 + ii, pc);
 #pragma unroll
-          for (int j = 0; j < 8; ++j) phi[j] = bj[jj][j] * bi[j];
+            for (int jj = 0; jj < NJ; ++jj) {
+              half8_t phi;
 #pragma unroll
-          for (int vb = 0; vb < 2; ++vb) acc[ii][jj][vb] = mfma32(phi, vv[vb], acc[ii][jj][vb]);
+              for (int j = 0; j < 8; ++j) phi[j] = bj[jj][j] * bi[j];
+#pragma unroll
+              for (int vb = 0; vb < 2; ++vb) acc[ii][jj][vb] = mfma32(phi, vv[vb], acc[ii][jj][vb]);
+            }
+          }
         }
-      }
-    });
-    // fp16 shadow of state_{c+1} for the applies of the next launch.
-    half_t* sh = reinterpret_cast<half_t*>(ws + kQuadShadow) + size_t((c + 1) % NSLOT) * PD * PD * PD;
+      },
+      [&](int j) {
+        // fp16 shadow of state_{c+1} for the applies of the next launch.
+        const int c = c0 + j;
+        half_t* sh = reinterpret_cast<half_t*>(ws + kQuadShadow) + size_t((c + 1) % NSLOT) * PD * PD * PD;
 #pragma unroll
-    for (int ii = 0; ii < NI; ++ii)
+        for (int ii = 0; ii < NI; ++ii)
 #pragma unroll
-      for (int jj = 0; jj < NJ; ++jj)
+          for (int jj = 0; jj < NJ; ++jj)
 #pragma unroll
-        for (int vb = 0; vb < 2; ++vb) store_shadow_t(sh + size_t(i0 + ii) * PD * PD, acc[ii][jj][vb], JB0 + jj, vb);
-  }
+            for (int vb = 0; vb < 2; ++vb)
+              store_shadow_t(sh + size_t(i0 + ii) * PD * PD, acc[ii][jj][vb], JB0 + jj, vb);
+      });
 #pragma unroll
   for (int ii = 0; ii < NI; ++ii)
 #pragma unroll
@@ -561,15 +630,13 @@ __device__ void quad_update_body(const PolyArgs& a, char* ws, int b, int h, int 
 // Quad-update workgroups 0..3: i < 32, two slices per wave, both j-blocks;
 // workgroups 4..5: i >= 32, four slices per wave, j >= 32 only -- the same
 // MFMA count per wave.
-template <typename T>
-__device__ void quad_update_role(const PolyArgs& a, char* ws, int b, int h, int ug, char* smem) {
+__device__ __forceinline__ void quad_update_role(const PolyArgs& a, char* ws, int ug, char* smem) {
   const int w = threadIdx.x / kWave;
-  if (ug < 4) quad_update_body<T, 2, 0>(a, ws, b, h, 8 * ug + 2 * w, smem);
-  else quad_update_body<T, 4, 1>(a, ws, b, h, 32 + 16 * (ug - 4) + 4 * w, smem);
+  if (ug < 4) quad_update_body<2, 0>(a, ws, 8 * ug + 2 * w, smem);
+  else quad_update_body<4, 1>(a, ws, 32 + 16 * (ug - 4) + 4 * w, smem);
 }
 
-template <typename T>
-__device__ void small_update_role(const PolyArgs& a, char* ws, int b, int h, char* smem) {
+__device__ __forceinline__ void small_update_role(const PolyArgs& a, char* ws, char* smem) {
   int c0, c1;
   update_range(a, c0, c1);
   if (c0 >= c1) return;
@@ -590,55 +657,65 @@ __device__ void small_update_role(const PolyArgs& a, char* ws, int b, int h, cha
     z = zs[lane];
     cs = zs[64 + lane];
   }
-  for (int c = c0; c < c1; ++c) {
-    float zsum = 0.f, csum = 0.f;
-    stream_tokens<T>(a, b, h, c * PC, min(a.S, c * PC + PC), smem, [&](half_t (*bt)[LP], half_t (*vt)[LP], int tk) {
-      const int t = tk + 8 * hl;
-      if (w == 0) {  // S_lin[j][v] = sum_t b_tj v_tv
+  float zsum = 0.f, csum = 0.f;
+  const char* tok = ws + kTokImg + size_t(a.launch & 1) * kTokImgBytes;
+  stream_image(
+      tok, c1 - c0, smem,
+      [&](const half_t* bT, const half_t* vT) {
 #pragma unroll
-        for (int jb = 0; jb < 2; ++jb) {
-          const half8_t bj = *reinterpret_cast<const half8_t*>(&bt[32 * jb + ln][t]);
+        for (int ks = 0; ks < 4; ++ks) {
+          const int pc = 2 * ks + hl;
+          if (w == 0) {  // S_lin[j][v] = sum_t b_tj v_tv
 #pragma unroll
-          for (int vb = 0; vb < 2; ++vb)
-            acc[jb][vb] = mfma32(bj, *reinterpret_cast<const half8_t*>(&vt[32 * vb + ln][t]), acc[jb][vb]);
+            for (int jb = 0; jb < 2; ++jb) {
+              const half8_t bj = img_piece(bT, 32 * jb + ln, pc);
+#pragma unroll
+              for (int vb = 0; vb < 2; ++vb) acc[jb][vb] = mfma32(bj, img_piece(vT, 32 * vb + ln, pc), acc[jb][vb]);
+            }
+          } else if (w == 1) {  // G[i][j] = sum_t b_ti b_tj
+#pragma unroll
+            for (int ib = 0; ib < 2; ++ib) {
+              const half8_t bi = img_piece(bT, 32 * ib + ln, pc);
+#pragma unroll
+              for (int jb = 0; jb < 2; ++jb) acc[ib][jb] = mfma32(bi, img_piece(bT, 32 * jb + ln, pc), acc[ib][jb]);
+            }
+          } else if (w == 2) {  // z[d] and S_const[d]: lane = dim, 16 tokens per step
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+              const half8_t bx = img_piece(bT, lane, 2 * ks + half);
+              const half8_t vx = img_piece(vT, lane, 2 * ks + half);
+#pragma unroll
+              for (int j = 0; j < 8; ++j) {
+                zsum += (float)bx[j];
+                csum += (float)vx[j];
+              }
+            }
+          }
         }
-      } else if (w == 1) {  // G[i][j] = sum_t b_ti b_tj
-#pragma unroll
-        for (int ib = 0; ib < 2; ++ib) {
-          const half8_t bi = *reinterpret_cast<const half8_t*>(&bt[32 * ib + ln][t]);
+      },
+      [&](int j) {
+        const int nxt = (c0 + j + 1) % NSLOT;
+        if (w == 0) {
+          half_t* sh = reinterpret_cast<half_t*>(ws + kLinShadow) + size_t(nxt) * PD * PD;  // [v][j]
 #pragma unroll
           for (int jb = 0; jb < 2; ++jb)
-            acc[ib][jb] = mfma32(bi, *reinterpret_cast<const half8_t*>(&bt[32 * jb + ln][t]), acc[ib][jb]);
+#pragma unroll
+            for (int vb = 0; vb < 2; ++vb) store_shadow_t(sh, acc[jb][vb], jb, vb);
+        } else if (w == 1) {
+          half_t* sh = reinterpret_cast<half_t*>(ws + kGramShadow) + size_t(nxt) * PD * PD;  // symmetric
+#pragma unroll
+          for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+            for (int jb = 0; jb < 2; ++jb) store_shadow_t(sh, acc[ib][jb], ib, jb);
+        } else if (w == 2) {
+          z += zsum;
+          cs += csum;
+          zsum = csum = 0.f;
+          float* zsh = reinterpret_cast<float*>(ws + kZsShadow) + nxt * 128;
+          zsh[lane] = z;
+          zsh[64 + lane] = cs;
         }
-      } else if (w == 2) {  // z[d] and S_const[d]: lane = dim, 16 tokens per step
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          zsum += (float)bt[lane][tk + j];
-          csum += (float)vt[lane][tk + j];
-        }
-      }
-    });
-    const int nxt = (c + 1) % NSLOT;
-    if (w == 0) {
-      half_t* sh = reinterpret_cast<half_t*>(ws + kLinShadow) + size_t(nxt) * PD * PD;  // [v][j]
-#pragma unroll
-      for (int jb = 0; jb < 2; ++jb)
-#pragma unroll
-        for (int vb = 0; vb < 2; ++vb) store_shadow_t(sh, acc[jb][vb], jb, vb);
-    } else if (w == 1) {
-      half_t* sh = reinterpret_cast<half_t*>(ws + kGramShadow) + size_t(nxt) * PD * PD;  // symmetric
-#pragma unroll
-      for (int ib = 0; ib < 2; ++ib)
-#pragma unroll
-        for (int jb = 0; jb < 2; ++jb) store_shadow_t(sh, acc[ib][jb], ib, jb);
-    } else if (w == 2) {
-      z += zsum;
-      cs += csum;
-      float* zsh = reinterpret_cast<float*>(ws + kZsShadow) + nxt * 128;
-      zsh[lane] = z;
-      zsh[64 + lane] = cs;
-    }
-  }
+      });
   if (w == 0) {
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb)
@@ -655,29 +732,60 @@ __device__ void small_update_role(const PolyArgs& a, char* ws, int b, int h, cha
   }
 }
 
-// Roles of one head in launch L: KG * NAPPLY apply workgroups (chunk
-// KG (L-1) + 1 + j / NAPPLY, row block j % NAPPLY; launch 0 applies chunk 0
-// only), NUPD quad-update workgroups and one small-state update, the updates
-// folding in chunks [KG L, KG L + KG).
+// Token images of the chunks the next launch folds in, [KG (L+1), KG (L+1) +
+// KG): chunk j of them by workgroup j, eight 64-token tiles, loads of the next
+// tile in flight while the current one is stored.
+template <typename T>
+__device__ void image_role(const PolyArgs& a, char* ws, int b, int h, int j) {
+  const int cn = KG * (a.launch + 1);
+  const int c = cn + j;
+  if (c >= min(cn + KG, a.n_chunks - 1)) return;
+  char* dst = ws + kTokImg + size_t((a.launch + 1) & 1) * kTokImgBytes + size_t(j) * (PC / 64) * kTileImg;
+  const int tid = threadIdx.x;
+  TokTile<T> x0, x1;
+  x0.init(a, b, h, tid);
+  x1.init(a, b, h, tid);
+  x0.load(c * PC);
+#pragma unroll
+  for (int blk = 0; blk < PC / 64; blk += 2) {
+    x1.load(c * PC + 64 * (blk + 1));
+    x0.store_image(dst + blk * kTileImg, a.rs, tid);
+    if (blk + 2 < PC / 64) x0.load(c * PC + 64 * (blk + 2));
+    x1.store_image(dst + (blk + 1) * kTileImg, a.rs, tid);
+  }
+}
+
+// Roles of one head in launch L: NUPD quad-update workgroups and one
+// small-state update folding in chunks [KG L, KG L + KG); KG * NAPPLY apply
+// workgroups (chunk KG (L-1) + 1 + j / NAPPLY, row block j % NAPPLY; launch 0
+// applies chunk 0 only); NCONV workgroups writing the token images of the
+// chunks launch L + 1 folds in. Launch -1 writes only the images for launch 0.
+// Head m runs on XCD m % 8 (its roles share that L2); each XCD issues the
+// roles of its heads role-major in that order, longest first.
 template <typename T>
 __global__ __launch_bounds__(PT, 2) void poly_chunk_kernel(PolyArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[kSmemBytes];
-  const int id = blockIdx.x;
-  const int logical = (id % kNumXcd) * a.per_xcd + id / kNumXcd;
-  if (logical >= a.total) return;
-  const int m = logical / NROLE;
-  const int role = logical % NROLE;
+  const int x = blockIdx.x % kNumXcd, k = blockIdx.x / kNumXcd;
+  const int nh = x < a.M ? (a.M - x + kNumXcd - 1) / kNumXcd : 0;  // heads on this XCD
+  if (k >= nh * NROLE) return;
+  const int rr = k / nh;
+  const int m = x + kNumXcd * (k % nh);
   if (a.flags != nullptr && a.flags[m] == 0) return;
   const int b = m / a.H, h = m % a.H;
   char* ws = a.ws + size_t(m) * kPerHead;
-  if (role < KG * NAPPLY) {
+  if (rr >= NUPD + 1 + KG * NAPPLY) {
+    image_role<T>(a, ws, b, h, rr - (NUPD + 1 + KG * NAPPLY));
+  } else if (a.launch < 0) {
+    return;
+  } else if (rr < NUPD) {
+    quad_update_role(a, ws, rr, smem);
+  } else if (rr == NUPD) {
+    small_update_role(a, ws, smem);
+  } else {
+    const int role = rr - (NUPD + 1);
     const int g = role / NAPPLY;
     const int c = a.launch == 0 ? (g == 0 ? 0 : -1) : KG * (a.launch - 1) + 1 + g;
     if (c >= 0 && c < a.n_chunks) apply_role<T>(a, ws, b, h, m, c, role % NAPPLY, smem);
-  } else if (role < KG * NAPPLY + NUPD) {
-    quad_update_role<T>(a, ws, b, h, role - KG * NAPPLY, smem);
-  } else {
-    small_update_role<T>(a, ws, b, h, smem);
   }
 }
 
@@ -691,6 +799,12 @@ int run(PolyArgs a, size_t ws_bytes, hipStream_t stream) {
   hipLaunchKernelGGL(zero_kernel, dim3(1024), dim3(256), 0, stream, reinterpret_cast<float4_t*>(a.ws),
                      ws_bytes / 16);
   if (hipGetLastError() != hipSuccess) return TJ_ERR_LAUNCH;
+  const dim3 grid(unsigned(kNumXcd * ((a.M + kNumXcd - 1) / kNumXcd) * NROLE));
+  if (a.n_chunks > 1) {  // token images of the chunks launch 0 folds in
+    a.launch = -1;
+    hipLaunchKernelGGL(poly_chunk_kernel<T>, grid, dim3(PT), 0, stream, a);
+    if (hipGetLastError() != hipSuccess) return TJ_ERR_LAUNCH;
+  }
   // Launch L applies chunks (KG (L-1), KG L] and folds in chunks [KG L, KG L + KG).
   const int n_launch = 1 + (a.n_chunks - 1 + KG - 1) / KG;
   for (int L = 0; L < n_launch; ++L) {
@@ -699,7 +813,7 @@ int run(PolyArgs a, size_t ws_bytes, hipStream_t stream) {
     const bool updates = KG * L < a.n_chunks - 1;
     if (!emits && !updates) continue;
     a.launch = L;
-    hipLaunchKernelGGL(poly_chunk_kernel<T>, dim3(a.per_xcd * kNumXcd), dim3(PT), 0, stream, a);
+    hipLaunchKernelGGL(poly_chunk_kernel<T>, grid, dim3(PT), 0, stream, a);
     if (hipGetLastError() != hipSuccess) return TJ_ERR_LAUNCH;
   }
   return TJ_OK;
@@ -726,7 +840,7 @@ extern "C" int tj_poly_attn_fwd(const void* q, const void* k, const void* v, voi
   if (B < 0 || H <= 0 || S < 0 || D <= 0 || chunk <= 0 || exact_prefix < 0 || !(scale > 0.f)) return TJ_ERR_SHAPE;
   if (D != tj::PD || chunk != tj::PC) return TJ_ERR_UNSUPPORTED;
   if (B == 0 || S == 0 || exact_prefix >= S) return TJ_OK;
-  if (B * H * tj::NROLE >= (int64_t(1) << 31) || S >= (int64_t(1) << 30)) return TJ_ERR_SHAPE;
+  if ((B * H + tj::kNumXcd) * tj::NROLE >= (int64_t(1) << 31) || S >= (int64_t(1) << 30)) return TJ_ERR_SHAPE;
   if (!q || !k || !v || !o || !coeffs) return TJ_ERR_SHAPE;
   if (!tjh::view_ok(q, q_strides, dtype) || !tjh::view_ok(k, k_strides, dtype) ||
       !tjh::view_ok(v, v_strides, dtype) || !tjh::view_ok(o, o_strides, dtype))
@@ -751,8 +865,7 @@ extern "C" int tj_poly_attn_fwd(const void* q, const void* k, const void* v, voi
   a.coeffs = coeffs;
   a.flags = flags;
   a.ws = static_cast<char*>(workspace);
-  a.total = (int)(B * H) * tj::NROLE;
-  a.per_xcd = (a.total + tj::kNumXcd - 1) / tj::kNumXcd;
+  a.M = (int)(B * H);
   a.n_chunks = (int)((S + tj::PC - 1) / tj::PC);
   if (dtype == TJ_F32) return tj::run<float>(a, need, stream);
   return tj::run<half_t>(a, need, stream);
