@@ -459,7 +459,10 @@ __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int 
 // of three LDS stages by direct global->LDS copies issued two tiles ahead (no
 // registers held). body(bT, vT) runs on every 64-token tile (b^T and v^T, 64
 // dim rows of 128 bytes with XOR-placed 16-byte pieces, see img_piece);
-// chunk_end(j) after the last tile of the launch's j-th chunk. The stages are
+// chunk_end(j) after the last tile of the launch's j-th chunk, once the
+// workgroup has passed that tile's barrier: its global stores then complete
+// under the next tile instead of holding up the wait for the copies (issued
+// before them) that the barrier needs. The stages are
 // distinct members addressed with compile-time indices, so the compiler can
 // tell the copies into one stage from the reads of another.
 struct TokRing {
@@ -511,8 +514,8 @@ __device__ __forceinline__ void stream_image(const char* img, int n_chunk, char*
     if (t + 2 < n) issue(t + 2, std::integral_constant<int, (sv + 2) % 3>{});
     const char* base = stage_ptr(st);
     body(reinterpret_cast<const half_t*>(base), reinterpret_cast<const half_t*>(base + PD * 128));
-    if ((t + 1) % kTiles == 0) chunk_end(t / kTiles);
     wait_next(t);
+    if ((t + 1) % kTiles == 0) chunk_end(t / kTiles);
   };
   if (n == 0) return;
   issue(0, std::integral_constant<int, 0>{});
