@@ -61,7 +61,7 @@ constexpr size_t kQuadImgBytes = size_t(PD) * 4 * 64 * 16 * 4;  // 1 MiB
 constexpr size_t kLinImg = kQuadImg + kQuadImgBytes;             // fp32 [2 jb][2 vb][64][16]
 constexpr size_t kGramImg = kLinImg + 4 * 64 * 16 * 4;           // fp32 [2 ib][2 jb][64][16]
 constexpr size_t kZsMaster = kGramImg + 4 * 64 * 16 * 4;         // fp32 z[64], S_const[64]
-constexpr size_t kQuadShadow = kZsMaster + 128 * 4;              // fp16 [NSLOT][64 i][64 v][64 j]
+constexpr size_t kQuadShadow = kZsMaster + 128 * 4;              // fp16 [NSLOT][64 i][8 q][64 v][8 j]
 constexpr size_t kLinShadow = kQuadShadow + NSLOT * size_t(PD) * PD * PD * 2;  // fp16 [NSLOT][64 v][64 j]
 constexpr size_t kGramShadow = kLinShadow + NSLOT * PD * PD * 2;  // fp16 [NSLOT][64][64] (symmetric)
 constexpr size_t kZsShadow = kGramShadow + NSLOT * PD * PD * 2;   // fp32 [NSLOT][128]
@@ -207,6 +207,15 @@ __device__ __forceinline__ half8_t mul8(half8_t x, half_t s) {
   return r;
 }
 
+// f(integral_constant<int, I>) for I = B .. E-1, each with compile-time I.
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Apply role: rows [row0, row0 + 128) of the chunk.
 // ---------------------------------------------------------------------------
@@ -245,16 +254,19 @@ __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int 
   }
 
   const half_t* qshadow = reinterpret_cast<const half_t*>(ws + kQuadShadow) + size_t(slot) * PD * PD * PD;
-  // The quad state streams through a ring of kRing LDS stages by direct
-  // global->LDS copies, two stages ahead of the MFMAs (no registers held).
-  // The stages are distinct members, addressed with compile-time stage
-  // indices, so the compiler can tell the copies into one stage from reads of
-  // another and does not wait for every copy in flight.
-  // Stage layout: [ii][v][64 j] rows of 128 bytes whose eight 16-byte pieces
-  // are XOR-swizzled by (v >> 1) & 7, so that 16 lanes reading one piece
-  // column of 16 consecutive rows touch 16 distinct bank groups.
-  // Copy instruction `it` of wave w fills 1 KiB slot (4 it + w) of the stage;
-  // lane l fills 16-byte piece slot 64 (4 it + w) + l.
+  // The fp16 quad shadow of one i is piece-major, [8 q][64 v][8 j]: piece q
+  // holds columns j = 8q .. 8q + 7 of every row v (1 KiB contiguous per q).
+  // It streams through a ring of kRing LDS stages by direct global->LDS
+  // copies two stages ahead of the MFMAs (no registers held). Pair p
+  // (i = 2p, 2p + 1) only reads the pieces q >= 2 ib, ib = p >> 3 (S is
+  // symmetric, see step), so its stage holds np = 8 - 2 ib piece columns of
+  // both i as [q - 2 ib][ii][64 v] 16-byte pieces (1 KiB per (q, ii)),
+  // filled by 2 np copy instructions (k = 2 (q - 2 ib) + ii; wave w issues
+  // k = w, w + 4, ...): 37.5 % fewer bytes than whole rows, and 16 lanes
+  // reading one piece column of 16 consecutive rows touch 256 contiguous
+  // bytes. The stages are distinct members addressed with compile-time
+  // indices, so the compiler can tell the copies into one stage from reads
+  // of another and does not wait for every copy in flight.
   struct Ring {
     char s0[kRingStage];
     char s1[kRingStage];
@@ -267,20 +279,17 @@ __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int 
     else if constexpr (decltype(st)::value == 1) return ring.s1;
     else return ring.s2;
   };
-  auto issue = [&](int pair, auto st) {
+  auto issue = [&](auto pc, auto st) {
+    constexpr int p = decltype(pc)::value;
+    constexpr int np = 8 - 2 * (p >> 3);
     char* base = stage_ptr(st);
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int slot = (4 * it + w) * 64 + lane;
-      const int ii = slot >> 9, vrow = (slot >> 3) & 63, pos = slot & 7;
-      // Pieces below the pair's diagonal 16-block are never read (S is
-      // symmetric, see step): those lanes re-read the first needed piece of
-      // the row -- no new lines fetched, every lane active, so the ring's
-      // wait counts stay exact.
-      const int piece = max(pos ^ ((vrow >> 1) & 7), 2 * (pair >> 3));
-      const half_t* src = qshadow + (size_t(2 * pair + ii) * PD + vrow) * PD + 8 * piece;
+    for (int it = 0; it < np / 2; ++it) {
+      const int k = w + 4 * it;
+      const int q = 2 * (p >> 3) + (k >> 1), ii = k & 1;
+      const half_t* src = qshadow + (size_t(2 * p + ii) * 8 + q) * (PD * 8) + lane * 8;
       __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                       (__attribute__((address_space(3))) void*)(base + (4 * it + w) * 1024), 16, 0, 0);
+                                       (__attribute__((address_space(3))) void*)(base + k * 1024), 16, 0, 0);
     }
   };
 
@@ -291,52 +300,48 @@ __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int 
     for (int r = 0; r < 16; ++r) accq[vb][r] = 0.f;
 
   constexpr int kPairs = PD / 2;
-  // One ring step: MFMAs on pair p from stage st, after issuing pair p + 2.
-  auto step = [&](int p, auto st) {
-    constexpr int sv = decltype(st)::value;
-    if (p + 2 < kPairs) issue(p + 2, std::integral_constant<int, (sv + 2) % kRing>{});
-    const char* base = stage_ptr(st);
+  // One ring step: MFMAs on pair p from its stage, after issuing pair p + 2.
+  auto step = [&](auto pc) {
+    constexpr int p = decltype(pc)::value;
+    constexpr int ib = p >> 3;  // 16-block of i = 2p, 2p + 1
+    using St = std::integral_constant<int, p % kRing>;
+    if constexpr (p + 2 < kPairs) issue(std::integral_constant<int, p + 2>{}, std::integral_constant<int, (p + 2) % kRing>{});
+    const char* base = stage_ptr(St{});
     // phi2(a).S = sum_i a_i sum_j a_j S_ij with S_ij = S_ji (the update forms
     // both from the same fp16 products b_i b_j in the same order): the j-block
     // holding i counts once, j-blocks above it twice (a_i doubled, exact in
     // fp16), j-blocks below it not at -- 37.5 % fewer MFMAs.
-    const int ib = p >> 3;  // 16-block of i = 2p, 2p + 1
 #pragma unroll
     for (int ii = 0; ii < 2; ++ii) {
       const half_t ai = at[qrow][2 * p + ii];
       const half_t ai2 = ai + ai;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        if (ks < ib) continue;
+      for (int ks = ib; ks < 4; ++ks) {
         const half8_t bop = mul8(aB[ks], ks == ib ? ai : ai2);
+        const int k = 2 * (2 * ks + hl - 2 * ib) + ii;
 #pragma unroll
         for (int vb = 0; vb < 2; ++vb) {
-          const int row = 32 * vb + ln, piece = 2 * ks + hl;
-          const half8_t sa = *reinterpret_cast<const half8_t*>(base + ii * (kRingStage / 2) + row * 128 +
-                                                               16 * (piece ^ ((row >> 1) & 7)));
+          const half8_t sa = *reinterpret_cast<const half8_t*>(base + k * 1024 + (32 * vb + ln) * 16);
           accq[vb] = mfma32(sa, bop, accq[vb]);
         }
       }
     }
     // Pair p + 1 (this wave's copies) must have landed before the barrier;
-    // pair p + 2 may stay in flight. A plain barrier: __syncthreads() would
-    // also wait for every copy in flight.
-    if (p + 2 < kPairs) __builtin_amdgcn_s_waitcnt(0x0074);  // vmcnt(4) lgkmcnt(0)
-    else __builtin_amdgcn_s_waitcnt(0x0070);                 // vmcnt(0) lgkmcnt(0)
+    // pair p + 2 (np (p + 2) / 2 copies of this wave) may stay in flight. A
+    // plain barrier: __syncthreads() would also wait for every copy in flight.
+    if constexpr (p + 2 < kPairs) {
+      constexpr int in_flight = (8 - 2 * ((p + 2) >> 3)) / 2;
+      __builtin_amdgcn_s_waitcnt(0x0070 | in_flight);  // vmcnt(in_flight) lgkmcnt(0)
+    } else {
+      __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+    }
     lds_barrier();
   };
-  issue(0, std::integral_constant<int, 0>{});
-  issue(1, std::integral_constant<int, 1>{});
-  __builtin_amdgcn_s_waitcnt(0x0074);  // pair 0 landed; a tile stores done
+  issue(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+  issue(std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
+  __builtin_amdgcn_s_waitcnt(0x0074);  // pair 0 landed (pair 1: four copies in flight); a tile stores done
   lds_barrier();
-  for (int p = 0; p + 3 <= kPairs; p += 3) {
-    step(p, std::integral_constant<int, 0>{});
-    step(p + 1, std::integral_constant<int, 1>{});
-    step(p + 2, std::integral_constant<int, 2>{});
-  }
-  static_assert(kPairs % 3 == 2, "tail below handles two pairs");
-  step(kPairs - 2, std::integral_constant<int, 0>{});
-  step(kPairs - 1, std::integral_constant<int, 1>{});
+  static_for<0, kPairs>(step);
 
   // Linear numerator term S_lin^T a^T and the quadratic denominator G a^T
   // (operands straight from the L2-resident shadows).
@@ -557,6 +562,18 @@ __device__ __forceinline__ void store_shadow_t(half_t* dst, const float16_t& acc
   }
 }
 
+// The same block written into the piece-major quad shadow of S_i,
+// [8 q][64 v][8 j] (q = j / 8), as the apply's ring reads it.
+__device__ __forceinline__ void store_quad_shadow(half_t* dst, const float16_t& acc, int rb, int cb) {
+  const int lane = threadIdx.x % kWave, hl = lane / 32, ln = lane % 32;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int j = 32 * rb + 8 * g + 4 * hl;  // four consecutive j, one piece
+    *reinterpret_cast<half4_t*>(dst + ((j >> 3) * 64 + 32 * cb + ln) * 8 + (j & 7)) =
+        half4_t{(half_t)acc[4 * g], (half_t)acc[4 * g + 1], (half_t)acc[4 * g + 2], (half_t)acc[4 * g + 3]};
+  }
+}
+
 // Chunks whose states this launch folds in: [c0, c1) (the final chunk's
 // update is never needed).
 __device__ __forceinline__ void update_range(const PolyArgs& a, int& c0, int& c1) {
@@ -620,7 +637,7 @@ __device__ __forceinline__ void quad_update_body(const PolyArgs& a, char* ws, in
           for (int jj = 0; jj < NJ; ++jj)
 #pragma unroll
             for (int vb = 0; vb < 2; ++vb)
-              store_shadow_t(sh + size_t(i0 + ii) * PD * PD, acc[ii][jj][vb], JB0 + jj, vb);
+              store_quad_shadow(sh + size_t(i0 + ii) * PD * PD, acc[ii][jj][vb], JB0 + jj, vb);
       });
 #pragma unroll
   for (int ii = 0; ii < NI; ++ii)
