@@ -169,6 +169,8 @@ def extreme(args, dev):
         "workload": "extreme-length attention core: guarded degree-2 polynomial attention, "
                     "B=4 S=65536 H=16 D=64, fp32 io, 60 polynomial heads + 4 exact fallback heads",
         "batch": b, "seq_len": s, "heads": h, "head_dim": d, "chunk": 512, "exact_prefix": 4096,
+        "data": "synthetic: q, k ~ N(0, 0.5^2), v ~ N(0, 1), head 0 of each sample q, k ~ N(0, 2^2), "
+                "generated on the GPU (seed 101234)",
     }
     return step, b * s, flops, bytes_alg, config, "poly_extreme_b4_s65536_h16_d64.md"
 
