@@ -259,14 +259,15 @@ __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int 
   // It streams through a ring of kRing LDS stages by direct global->LDS
   // copies two stages ahead of the MFMAs (no registers held). Pair p
   // (i = 2p, 2p + 1) only reads the pieces q >= 2 ib, ib = p >> 3 (S is
-  // symmetric, see step), so its stage holds np = 8 - 2 ib piece columns of
-  // both i as [q - 2 ib][ii][64 v] 16-byte pieces (1 KiB per (q, ii)),
-  // filled by 2 np copy instructions (k = 2 (q - 2 ib) + ii; wave w issues
-  // k = w, w + 4, ...): 37.5 % fewer bytes than whole rows, and 16 lanes
-  // reading one piece column of 16 consecutive rows touch 256 contiguous
-  // bytes. The stages are distinct members addressed with compile-time
-  // indices, so the compiler can tell the copies into one stage from reads
-  // of another and does not wait for every copy in flight.
+  // symmetric, see the step), np = 8 - 2 ib of them per row, so a stage holds
+  // G pairs (G = 1, 1, 2, 4 for ib = 0 .. 3, at most 16 KiB) as
+  // [gp][q - 2 ib][ii][64 v] 16-byte pieces (1 KiB per (gp, q, ii)), filled
+  // by 2 G np copy instructions (k = 2 (gp np + q - 2 ib) + ii; wave w issues
+  // k = w, w + 4, ...): 37.5 % fewer bytes than whole rows, 22 stages instead
+  // of 32, and 16 lanes reading one piece column of 16 consecutive rows touch
+  // 256 contiguous bytes. The stages are distinct members addressed with
+  // compile-time indices, so the compiler can tell the copies into one stage
+  // from reads of another and does not wait for every copy in flight.
   struct Ring {
     char s0[kRingStage];
     char s1[kRingStage];
@@ -279,15 +280,20 @@ __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int 
     else if constexpr (decltype(st)::value == 1) return ring.s1;
     else return ring.s2;
   };
-  auto issue = [&](auto pc, auto st) {
-    constexpr int p = decltype(pc)::value;
-    constexpr int np = 8 - 2 * (p >> 3);
+  constexpr int kSteps = 22;
+  auto step_p0 = [](int st) constexpr { return st < 16 ? st : (st < 20 ? 16 + 2 * (st - 16) : 24 + 4 * (st - 20)); };
+  auto step_g = [](int st) constexpr { return st < 16 ? 1 : (st < 20 ? 2 : 4); };
+  auto issue = [&](auto sc, auto st) {
+    constexpr int p0 = step_p0(decltype(sc)::value), G = step_g(decltype(sc)::value);
+    constexpr int ib = p0 >> 3, np = 8 - 2 * ib;
+    static_assert(G * np * 2 <= 16, "a stage holds at most 16 KiB");
     char* base = stage_ptr(st);
 #pragma unroll
-    for (int it = 0; it < np / 2; ++it) {
+    for (int it = 0; it < G * np / 2; ++it) {
       const int k = w + 4 * it;
-      const int q = 2 * (p >> 3) + (k >> 1), ii = k & 1;
-      const half_t* src = qshadow + (size_t(2 * p + ii) * 8 + q) * (PD * 8) + lane * 8;
+      const int gp = k / (2 * np), rem = k % (2 * np);
+      const int q = 2 * ib + (rem >> 1), ii = rem & 1;
+      const half_t* src = qshadow + (size_t(2 * (p0 + gp) + ii) * 8 + q) * (PD * 8) + lane * 8;
       __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
                                        (__attribute__((address_space(3))) void*)(base + k * 1024), 16, 0, 0);
     }
@@ -299,38 +305,41 @@ __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int 
 #pragma unroll
     for (int r = 0; r < 16; ++r) accq[vb][r] = 0.f;
 
-  constexpr int kPairs = PD / 2;
-  // One ring step: MFMAs on pair p from its stage, after issuing pair p + 2.
-  auto step = [&](auto pc) {
-    constexpr int p = decltype(pc)::value;
-    constexpr int ib = p >> 3;  // 16-block of i = 2p, 2p + 1
-    using St = std::integral_constant<int, p % kRing>;
-    if constexpr (p + 2 < kPairs) issue(std::integral_constant<int, p + 2>{}, std::integral_constant<int, (p + 2) % kRing>{});
-    const char* base = stage_ptr(St{});
+  // One ring step: MFMAs on the pairs of stage sc, after issuing stage sc + 2.
+  auto step = [&](auto sc) {
+    constexpr int si = decltype(sc)::value;
+    constexpr int p0 = step_p0(si), G = step_g(si);
+    constexpr int ib = p0 >> 3, np = 8 - 2 * ib;  // 16-block of every i of the stage
+    if constexpr (si + 2 < kSteps) issue(std::integral_constant<int, si + 2>{}, std::integral_constant<int, (si + 2) % kRing>{});
+    const char* base = stage_ptr(std::integral_constant<int, si % kRing>{});
     // phi2(a).S = sum_i a_i sum_j a_j S_ij with S_ij = S_ji (the update forms
     // both from the same fp16 products b_i b_j in the same order): the j-block
     // holding i counts once, j-blocks above it twice (a_i doubled, exact in
     // fp16), j-blocks below it not at -- 37.5 % fewer MFMAs.
 #pragma unroll
-    for (int ii = 0; ii < 2; ++ii) {
-      const half_t ai = at[qrow][2 * p + ii];
-      const half_t ai2 = ai + ai;
+    for (int gp = 0; gp < G; ++gp) {
+      const int p = p0 + gp;
 #pragma unroll
-      for (int ks = ib; ks < 4; ++ks) {
-        const half8_t bop = mul8(aB[ks], ks == ib ? ai : ai2);
-        const int k = 2 * (2 * ks + hl - 2 * ib) + ii;
+      for (int ii = 0; ii < 2; ++ii) {
+        const half_t ai = at[qrow][2 * p + ii];
+        const half_t ai2 = ai + ai;
 #pragma unroll
-        for (int vb = 0; vb < 2; ++vb) {
-          const half8_t sa = *reinterpret_cast<const half8_t*>(base + k * 1024 + (32 * vb + ln) * 16);
-          accq[vb] = mfma32(sa, bop, accq[vb]);
+        for (int ks = ib; ks < 4; ++ks) {
+          const half8_t bop = mul8(aB[ks], ks == ib ? ai : ai2);
+          const int k = 2 * (gp * np + 2 * ks + hl - 2 * ib) + ii;
+#pragma unroll
+          for (int vb = 0; vb < 2; ++vb) {
+            const half8_t sa = *reinterpret_cast<const half8_t*>(base + k * 1024 + (32 * vb + ln) * 16);
+            accq[vb] = mfma32(sa, bop, accq[vb]);
+          }
         }
       }
     }
-    // Pair p + 1 (this wave's copies) must have landed before the barrier;
-    // pair p + 2 (np (p + 2) / 2 copies of this wave) may stay in flight. A
-    // plain barrier: __syncthreads() would also wait for every copy in flight.
-    if constexpr (p + 2 < kPairs) {
-      constexpr int in_flight = (8 - 2 * ((p + 2) >> 3)) / 2;
+    // Stage sc + 1 (this wave's copies) must have landed before the barrier;
+    // stage sc + 2 (G np / 2 copies of this wave) may stay in flight. A plain
+    // barrier: __syncthreads() would also wait for every copy in flight.
+    if constexpr (si + 2 < kSteps) {
+      constexpr int in_flight = step_g(si + 2) * (8 - 2 * (step_p0(si + 2) >> 3)) / 2;
       __builtin_amdgcn_s_waitcnt(0x0070 | in_flight);  // vmcnt(in_flight) lgkmcnt(0)
     } else {
       __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
@@ -339,9 +348,9 @@ __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int 
   };
   issue(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
   issue(std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
-  __builtin_amdgcn_s_waitcnt(0x0074);  // pair 0 landed (pair 1: four copies in flight); a tile stores done
+  __builtin_amdgcn_s_waitcnt(0x0074);  // stage 0 landed (stage 1: four copies in flight); a tile stores done
   lds_barrier();
-  static_for<0, kPairs>(step);
+  static_for<0, kSteps>(step);
 
   // Linear numerator term S_lin^T a^T and the quadratic denominator G a^T
   // (operands straight from the L2-resident shadows).
