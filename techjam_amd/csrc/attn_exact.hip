@@ -190,7 +190,10 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
   const int ln = lane % 32;
   const int qw0 = q0 + WROWS * w;
 
-  const int kv_end = a.causal ? min(q0 + TROWS, L) : L;
+  // Rows [q0, row_end) need keys (rows in [L, row_cap) are written as zeros
+  // by the epilogue); a tile with none of them streams no keys at all.
+  const int row_end = min(min(q0 + TROWS, L), row_cap);
+  const int kv_end = q0 >= row_end ? 0 : (a.causal ? row_end : L);
   const int n_kv = kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
   // Last key this wave needs (inclusive); waves whose rows are all padding
   // (or beyond row_cap) compute nothing.
