@@ -92,6 +92,27 @@ int tj_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype,
                 hipStream_t stream);
 
 /*
+ * tj_attn_fwd with the projection biases of q and v folded in: the kernel
+ * reads the bias-free projections q', k', v' and computes the attention of
+ * q' + q_bias, k' + k_bias, v' + v_bias. A key bias never changes the output
+ * (it adds the same q.k_bias to every score of a row, and a row's softmax is
+ * invariant to that), so it has no argument; the value bias comes out as
+ * + v_bias on every valid row (a row's probabilities sum to 1). Padded rows
+ * stay zero. This saves the pass over the [B, S, 3D] projection output that
+ * adds its bias (the packed projection of sdpa.py:127-138 through
+ * torch.nn.Linear).
+ *
+ * q_bias, v_bias: device fp32 [H * D] (head h at h * D), 4-byte aligned, or
+ * NULL. No row limits or split scores on this entry point.
+ */
+int tj_attn_fwd_proj_bias(const void* q, const void* k, const void* v, void* o, int dtype,
+                          int64_t B, int64_t H, int64_t S, int64_t D,
+                          const int64_t q_strides[4], const int64_t k_strides[4],
+                          const int64_t v_strides[4], const int64_t o_strides[4],
+                          float scale, int causal, const int32_t* valid_len,
+                          const float* q_bias, const float* v_bias, hipStream_t stream);
+
+/*
  * Device-side score guard of the polynomial route.
  *
  * Replaces estimate_sigma / poly_is_safe / hermite_coefficients

@@ -52,6 +52,8 @@ struct AttnArgs {
   const int32_t* valid_len;
   const int32_t* row_limit;
   const int32_t* qk_split;
+  const float* q_bias;  // [H * D] fp32 or null: added to q before scaling
+  const float* v_bias;  // [H * D] fp32 or null: added to every valid output row
   int n_mtiles;
   int total_tiles;
   int per_xcd;
@@ -219,7 +221,8 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
           if (in) x.load(qp + base + d0 + e); else x.zero();
 #pragma unroll
           for (int j = 0; j < Vec16<T>::N; ++j) {
-            const float y = x.get(j) * a.qscale;
+            const float bq = a.q_bias != nullptr ? a.q_bias[h * HD + d0 + e + j] : 0.f;
+            const float y = (x.get(j) + bq) * a.qscale;
             const half_t hi = (half_t)y;
             qf[qb][ks][e + j] = hi;
             if constexpr (SPLIT) qlo[qb][ks][e + j] = (half_t)(y - (float)hi);
@@ -362,20 +365,23 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
     const int qi = qw0 + 32 * qb + ln;
     const float l_tot = pair_sum(l_run[qb]);
     if (qi < row_cap) {
-      const float inv = (qi < L && l_tot > 0.f) ? 1.f / l_tot : 0.f;
+      const bool valid = qi < L && l_tot > 0.f;
+      const float inv = valid ? 1.f / l_tot : 0.f;
+      // A value bias adds b_v to every valid row (its probabilities sum to 1).
+      const float* vb = (valid && a.v_bias != nullptr) ? a.v_bias + h * HD : nullptr;
       T* op = reinterpret_cast<T*>(a.o) + a.vo.row(b, h, qi);
 #pragma unroll
       for (int db = 0; db < TL::DB; ++db)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int d0 = db * 32 + 8 * g + 4 * hl;
+          float y[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) y[e] = oacc[qb][db][4 * g + e] * inv + (vb != nullptr ? vb[d0 + e] : 0.f);
           if constexpr (sizeof(T) == 4) {
-            *reinterpret_cast<float4_t*>(op + d0) = float4_t{oacc[qb][db][4 * g] * inv, oacc[qb][db][4 * g + 1] * inv,
-                                                              oacc[qb][db][4 * g + 2] * inv, oacc[qb][db][4 * g + 3] * inv};
+            *reinterpret_cast<float4_t*>(op + d0) = float4_t{y[0], y[1], y[2], y[3]};
           } else {
-            *reinterpret_cast<half4_t*>(op + d0) =
-                half4_t{(half_t)(oacc[qb][db][4 * g] * inv), (half_t)(oacc[qb][db][4 * g + 1] * inv),
-                        (half_t)(oacc[qb][db][4 * g + 2] * inv), (half_t)(oacc[qb][db][4 * g + 3] * inv)};
+            *reinterpret_cast<half4_t*>(op + d0) = half4_t{(half_t)y[0], (half_t)y[1], (half_t)y[2], (half_t)y[3]};
           }
         }
     }
@@ -465,12 +471,13 @@ int dispatch_hd(const AttnArgs& a, int64_t D, hipStream_t stream) {
 }  // namespace
 }  // namespace tj
 
-extern "C" int tj_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype,
-                           int64_t B, int64_t H, int64_t S, int64_t D,
-                           const int64_t q_strides[4], const int64_t k_strides[4],
-                           const int64_t v_strides[4], const int64_t o_strides[4],
-                           float scale, int causal, const int32_t* valid_len,
-                           const int32_t* row_limit, const int32_t* qk_split, hipStream_t stream) {
+namespace {
+
+int attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype, int64_t B, int64_t H, int64_t S,
+             int64_t D, const int64_t q_strides[4], const int64_t k_strides[4], const int64_t v_strides[4],
+             const int64_t o_strides[4], float scale, int causal, const int32_t* valid_len,
+             const int32_t* row_limit, const int32_t* qk_split, const float* q_bias, const float* v_bias,
+             hipStream_t stream) {
   if (dtype != TJ_F32 && dtype != TJ_F16) return TJ_ERR_DTYPE;
   if (B < 0 || H <= 0 || S < 0 || D <= 0) return TJ_ERR_SHAPE;
   if (B * H * ((S + 127) / 128) >= (int64_t(1) << 31) || S >= (int64_t(1) << 30)) return TJ_ERR_SHAPE;
@@ -480,6 +487,7 @@ extern "C" int tj_attn_fwd(const void* q, const void* k, const void* v, void* o,
   if (!tjh::view_ok(q, q_strides, dtype) || !tjh::view_ok(k, k_strides, dtype) ||
       !tjh::view_ok(v, v_strides, dtype) || !tjh::view_ok(o, o_strides, dtype))
     return TJ_ERR_ALIGN;
+  if ((reinterpret_cast<uintptr_t>(q_bias) | reinterpret_cast<uintptr_t>(v_bias)) & 3u) return TJ_ERR_ALIGN;
   // K and V rows of one (b, h) are addressed with 31-bit byte offsets.
   for (const int64_t* st : {k_strides, v_strides}) {
     if (st[2] < 0 || ((S - 1) * st[2] + D) * tjh::elem_size(dtype) >= (int64_t(1) << 31))
@@ -498,6 +506,30 @@ extern "C" int tj_attn_fwd(const void* q, const void* k, const void* v, void* o,
   a.valid_len = valid_len;
   a.row_limit = row_limit;
   a.qk_split = qk_split;
+  a.q_bias = q_bias;
+  a.v_bias = v_bias;
   if (dtype == TJ_F32) return tj::dispatch_hd<float>(a, D, stream);
   return tj::dispatch_hd<half_t>(a, D, stream);
+}
+
+}  // namespace
+
+extern "C" int tj_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype,
+                           int64_t B, int64_t H, int64_t S, int64_t D,
+                           const int64_t q_strides[4], const int64_t k_strides[4],
+                           const int64_t v_strides[4], const int64_t o_strides[4],
+                           float scale, int causal, const int32_t* valid_len,
+                           const int32_t* row_limit, const int32_t* qk_split, hipStream_t stream) {
+  return attn_fwd(q, k, v, o, dtype, B, H, S, D, q_strides, k_strides, v_strides, o_strides, scale, causal,
+                  valid_len, row_limit, qk_split, nullptr, nullptr, stream);
+}
+
+extern "C" int tj_attn_fwd_proj_bias(const void* q, const void* k, const void* v, void* o, int dtype,
+                                     int64_t B, int64_t H, int64_t S, int64_t D,
+                                     const int64_t q_strides[4], const int64_t k_strides[4],
+                                     const int64_t v_strides[4], const int64_t o_strides[4],
+                                     float scale, int causal, const int32_t* valid_len,
+                                     const float* q_bias, const float* v_bias, hipStream_t stream) {
+  return attn_fwd(q, k, v, o, dtype, B, H, S, D, q_strides, k_strides, v_strides, o_strides, scale, causal,
+                  valid_len, nullptr, nullptr, q_bias, v_bias, stream);
 }

@@ -23,6 +23,7 @@ from __future__ import annotations
 from typing import Optional
 
 import torch
+import torch.nn.functional as F
 
 from ..kernels.attention import scaled_dot_product_attention
 from ..model import HipSelfAttention, linear
@@ -35,8 +36,13 @@ class StridedSDPASelfAttention(HipSelfAttention):
 
     def context(self, x, valid_token_mask=None, causal=False, valid_len=None):
         b, s, _ = x.shape
-        q, k, v = self.project_qkv(x)
-        ctx = scaled_dot_product_attention(q, k, v, is_causal=causal, scale=self.scale, valid_len=valid_len)
+        if self.folds_biases(x):
+            q, k, v, qb, vb = self.project_qkv_folded(x)
+            ctx = scaled_dot_product_attention(q, k, v, is_causal=causal, scale=self.scale, valid_len=valid_len,
+                                               q_bias=qb, v_bias=vb)
+        else:
+            q, k, v = self.project_qkv(x)
+            ctx = scaled_dot_product_attention(q, k, v, is_causal=causal, scale=self.scale, valid_len=valid_len)
         return ctx.transpose(1, 2).reshape(b, s, self.d_model)
 
 
@@ -82,6 +88,16 @@ class PackedQKVSDPASelfAttention(StridedSDPASelfAttention):
         packed = linear(x, self._packed_qkv_weight, self._packed_qkv_bias)
         q, k, v = packed.view(b, s, 3, self.num_heads, self.head_dim).unbind(dim=2)
         return q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+
+    def project_qkv_folded(self, x: torch.Tensor):
+        """One bias-free ``[3D, D]`` GEMM; the q and v thirds of the packed bias
+        go to the kernel (the key third never changes the output)."""
+        b, s, _ = x.shape
+        packed = F.linear(x, self._packed_qkv_weight)
+        q, k, v = packed.view(b, s, 3, self.num_heads, self.head_dim).unbind(dim=2)
+        d = self.d_model
+        return (q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
+                self._packed_qkv_bias[:d], self._packed_qkv_bias[2 * d:])
 
 
 def attention_core(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool = True,

@@ -41,6 +41,11 @@ SIGNATURES = {
         [_vp, _vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _i64p, _i64p, _i64p, _i64p,
          _f32, _int, _vp, _vp, _vp, _vp],
     ),
+    "tj_attn_fwd_proj_bias": (
+        _int,
+        [_vp, _vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _i64p, _i64p, _i64p, _i64p,
+         _f32, _int, _vp, _vp, _vp, _vp],
+    ),
     "tj_score_guard": (
         _int,
         [_vp, _vp, _int, _i64, _i64, _i64, _i64, _i64p, _i64p, _f32, _vp, _i64, _f32, _i64,

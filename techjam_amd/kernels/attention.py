@@ -95,6 +95,8 @@ def scaled_dot_product_attention(
     row_limit: Optional[torch.Tensor] = None,
     qk_split: Union[bool, torch.Tensor, None] = None,
     out: Optional[torch.Tensor] = None,
+    q_bias: Optional[torch.Tensor] = None,
+    v_bias: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Exact attention on the HIP kernel; ``[B, H, S, D]`` views in, ``[B, H, S, D]`` out.
 
@@ -105,6 +107,12 @@ def scaled_dot_product_attention(
     other rows of ``out`` are left untouched. ``qk_split`` (``True`` for all
     heads, or an int32 ``[B*H]`` device flag tensor) selects the three-MFMA
     score path that keeps fp32-level score accuracy for wide score ranges.
+
+    ``q_bias`` / ``v_bias`` (fp32 ``[H*D]``, contiguous, on the device) are the
+    projection biases of bias-free q and v views: the result is the attention
+    of ``q + q_bias`` and ``v + v_bias``. A key bias has no effect on the
+    output (it shifts every score of a row by the same amount), so callers
+    drop it. Not combined with ``row_limit`` or ``qk_split``.
     """
     _check_qkv(q, k, v)
     dev = _require_device(q, k, v)
@@ -125,6 +133,22 @@ def scaled_dot_product_attention(
         if t is not None and (t.dtype != torch.int32 or t.device != dev or t.numel() != n
                               or not t.is_contiguous()):
             raise ValueError(f"{name} must be a contiguous int32 tensor of {n} elements on {dev}")
+    if q_bias is not None or v_bias is not None:
+        if row_limit is not None or qk_split is not None:
+            raise ValueError("q_bias / v_bias do not combine with row_limit or qk_split")
+        for name, t in (("q_bias", q_bias), ("v_bias", v_bias)):
+            if t is not None and (t.dtype != torch.float32 or t.device != dev or t.numel() != h * d
+                                  or not t.is_contiguous()):
+                raise ValueError(f"{name} must be a contiguous float32 tensor of {h * d} elements on {dev}")
+        code = _lib.lib().tj_attn_fwd_proj_bias(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), _DTYPES[q.dtype],
+            b, h, s, d,
+            _lib.strides4(q), _lib.strides4(k), _lib.strides4(v), _lib.strides4(out),
+            float(scale), int(bool(is_causal)), _ptr(valid_len), _ptr(q_bias), _ptr(v_bias),
+            _stream_ptr(dev),
+        )
+        _lib.check(code, "tj_attn_fwd_proj_bias")
+        return out
     code = _lib.lib().tj_attn_fwd(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), _DTYPES[q.dtype],
         b, h, s, d,

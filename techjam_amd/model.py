@@ -100,14 +100,30 @@ class HipSelfAttention(nn.Module):
     def project_qkv(self, x: torch.Tensor):
         return self.heads_view(self.q_proj(x)), self.heads_view(self.k_proj(x)), self.heads_view(self.v_proj(x))
 
+    def folds_biases(self, x: torch.Tensor) -> bool:
+        """Whether the q / v projection biases go to the kernel (inference on the GPU)."""
+        return (x.is_cuda and not torch.is_grad_enabled() and self.q_proj.bias is not None
+                and self.v_proj.bias is not None and self.q_proj.bias.dtype == torch.float32)
+
+    def project_qkv_folded(self, x: torch.Tensor):
+        """Bias-free q, k, v head views and the q / v biases the kernel adds
+        (a key bias never changes the attention output)."""
+        return (self.heads_view(F.linear(x, self.q_proj.weight)), self.heads_view(F.linear(x, self.k_proj.weight)),
+                self.heads_view(F.linear(x, self.v_proj.weight)), self.q_proj.bias, self.v_proj.bias)
+
     def attend(self, q, k, v, valid_len, causal):
         return scaled_dot_product_attention(q, k, v, is_causal=causal, scale=self.scale, valid_len=valid_len)
 
     def context(self, x, valid_token_mask=None, causal=False, valid_len=None):
         """Attention output before the output projection, ``[B, S, D]`` (a free view)."""
         b, s, _ = x.shape
-        q, k, v = self.project_qkv(x)
-        ctx = self.attend(q, k, v, valid_len, causal)
+        if self.folds_biases(x):
+            q, k, v, qb, vb = self.project_qkv_folded(x)
+            ctx = scaled_dot_product_attention(q, k, v, is_causal=causal, scale=self.scale, valid_len=valid_len,
+                                               q_bias=qb, v_bias=vb)
+        else:
+            q, k, v = self.project_qkv(x)
+            ctx = self.attend(q, k, v, valid_len, causal)
         return ctx.transpose(1, 2).reshape(b, s, self.d_model)
 
     def forward(self, x, valid_token_mask=None, causal=False, valid_len=None):

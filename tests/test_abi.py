@@ -57,6 +57,21 @@ def _strides(*s):
     return (ctypes.c_int64 * 4)(*s)
 
 
+def test_attn_proj_bias_rejects_bad_arguments_before_launching():
+    from techjam_amd.kernels import _lib
+
+    L = _lib.lib()
+    st = _strides(64 * 128 * 4, 64, 64 * 4, 1)
+    args = [16, 16, 16, 16]  # fake aligned pointers: never dereferenced on these paths
+    f = L.tj_attn_fwd_proj_bias
+    assert f(*args, 7, 1, 4, 128, 64, st, st, st, st, 0.125, 1, None, 16, 16, None) == _lib.TJ_ERR_DTYPE
+    assert f(*args, _lib.TJ_F32, 1, 4, 128, 48, st, st, st, st, 0.125, 1, None, 16, 16, None) == _lib.TJ_ERR_UNSUPPORTED
+    # bias pointers must be 4-byte aligned
+    assert f(*args, _lib.TJ_F32, 1, 4, 128, 64, st, st, st, st, 0.125, 1, None, 18, 16, None) == _lib.TJ_ERR_ALIGN
+    assert f(*args, _lib.TJ_F32, 1, 4, 128, 64, st, st, st, st, 0.125, 1, None, 16, 17, None) == _lib.TJ_ERR_ALIGN
+    assert f(*args, _lib.TJ_F32, 0, 4, 128, 64, st, st, st, st, 0.125, 1, None, 16, 16, None) == _lib.TJ_OK
+
+
 def test_attn_rejects_bad_arguments_before_launching():
     from techjam_amd.kernels import _lib
 

@@ -70,6 +70,31 @@ def test_right_padding_valid_lengths(cuda, causal):
         assert torch.count_nonzero(got[bi, :, n:]).item() == 0
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_projection_biases_folded_into_the_kernel(cuda, causal):
+    """q_bias / v_bias on bias-free projections equal attention of the biased
+    tensors; the key bias, which the kernel never sees, shifts whole score rows
+    and drops out of the softmax. Padded rows stay exact zeros."""
+    from techjam_amd.kernels import scaled_dot_product_attention
+
+    b, h, s, d = 3, 4, 300, 64
+    q, k, v = (_draw((b, h, s, d), seed) for seed in (31, 32, 33))
+    bq, bk, bv = (_draw((h, d), seed, scale=0.5) for seed in (34, 35, 36))
+    lengths = [300, 123, 0]
+    ref = brute_force_attention(q + bq[None, :, None], k + bk[None, :, None], v + bv[None, :, None],
+                                d ** -0.5, causal, valid_len=lengths)
+    vl = torch.tensor(lengths, dtype=torch.int32, device=cuda)
+    got = scaled_dot_product_attention(q.to(cuda), k.to(cuda), v.to(cuda), is_causal=causal, valid_len=vl,
+                                       q_bias=bq.reshape(-1).to(cuda), v_bias=bv.reshape(-1).to(cuda))
+    torch.cuda.synchronize()
+    _assert_close(got, ref, max_abs=4e-3, what=f"folded biases causal={causal}")
+    for bi, n in enumerate(lengths):
+        assert torch.count_nonzero(got[bi, :, n:]).item() == 0
+    with pytest.raises(ValueError):
+        scaled_dot_product_attention(q.to(cuda), k.to(cuda), v.to(cuda), q_bias=bq.reshape(-1).to(cuda),
+                                     row_limit=torch.zeros(b * h, dtype=torch.int32, device=cuda))
+
+
 def test_row_limit_leaves_other_rows_untouched(cuda):
     from techjam_amd.kernels import scaled_dot_product_attention
 
