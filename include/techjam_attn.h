@@ -247,6 +247,23 @@ int tj_bias_residual(float* out, const float* x, const float* y, const float* bi
  */
 int tj_bias_gelu(float* y, const float* bias, int64_t rows, int64_t cols, hipStream_t stream);
 
+/*
+ * tj_bias_residual (same modes, out may alias x or y) fused with the
+ * LayerNorm that reads its result next (torch_transformer_benchmark.py:140-145:
+ * norm2 after the attention residual, the next block's norm1 or the final norm
+ * after the FFN residual, :163-172):
+ *   ln_out[r,:] = (out[r,:] - mean) / sqrt(var + eps) * gamma + beta,
+ * mean and biased variance over the row, as torch.nn.LayerNorm defines them.
+ * With zero_ln_padded, rows at or past valid_len get ln_out = 0 (the final
+ * masked_fill). ln_out must not overlap out. cols must be 256, 512, 1024 or
+ * 2048 (TJ_ERR_UNSUPPORTED otherwise); all pointers 16-byte aligned.
+ */
+int tj_bias_residual_layernorm(float* out, float* ln_out, const float* x, const float* y,
+                               const float* bias, const float* gamma, const float* beta,
+                               int64_t rows, int64_t cols, int64_t seq_len,
+                               const int32_t* valid_len, int mode, float eps,
+                               int zero_ln_padded, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

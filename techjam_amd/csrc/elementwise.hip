@@ -7,6 +7,10 @@
 //                      out = row valid ? x + y + b : 0             (mode 2)
 //                      out = x + y + b                             (mode 0)
 //   tj_bias_gelu     : y = gelu(y + b), exact (erf) form, in place
+//   tj_bias_residual_layernorm : one of the residual forms above, and in the
+//                      same pass n = LayerNorm(out) (the next block's norm, or
+//                      the final one), so that the norm does not read the
+//                      residual stream again
 //
 // Tensors are fp32 [rows, cols] row-major with cols % 4 == 0 and 16-byte
 // aligned bases; row r = b * seq_len + s is valid iff s < valid_len[b].
@@ -56,6 +60,65 @@ __global__ __launch_bounds__(ET) void bias_gelu_kernel(float* y, const float* bi
   }
 }
 
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// One wave per row of N4 * 256 columns: lane l holds float4 columns l + 64 j.
+// The mean and the (biased) variance are two exact passes over the row held
+// in registers, as torch.nn.LayerNorm defines them.
+template <int N4>
+__global__ __launch_bounds__(ET) void bias_residual_ln_kernel(float* out, float* ln_out, const float* x, const float* y,
+                                                              const float* bias, const float* gamma, const float* beta,
+                                                              int64_t rows, int64_t seq_len, const int32_t* valid_len,
+                                                              int mode, float eps, int zero_ln_padded) {
+  const int lane = threadIdx.x % 64;
+  const int64_t row = blockIdx.x * (int64_t)(ET / 64) + threadIdx.x / 64;
+  if (row >= rows) return;
+  constexpr int C4 = N4 * 64;  // float4 columns per row
+  const bool ok = mode == 0 || row_valid(row, seq_len, valid_len);
+  const float4_t* xr = reinterpret_cast<const float4_t*>(x) + row * C4;
+  const float4_t* yr = reinterpret_cast<const float4_t*>(y) + row * C4;
+  float4_t r[N4];
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < N4; ++j) {
+    const int c = lane + 64 * j;
+    const float4_t xv = xr[c], yv = yr[c];
+    const float4_t bv = reinterpret_cast<const float4_t*>(bias)[c];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float t = yv[e] + bv[e];
+      r[j][e] = mode == 2 ? (ok ? xv[e] + t : 0.f) : xv[e] + (ok ? t : 0.f);
+      sum += r[j][e];
+    }
+    reinterpret_cast<float4_t*>(out)[row * C4 + c] = r[j];
+  }
+  const float mean = wave_sum(sum) / (float)(C4 * 4);
+  float sq = 0.f;
+#pragma unroll
+  for (int j = 0; j < N4; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float d = r[j][e] - mean;
+      sq += d * d;
+    }
+  const float rstd = 1.f / sqrtf(wave_sum(sq) / (float)(C4 * 4) + eps);
+  const bool zero = zero_ln_padded != 0 && !row_valid(row, seq_len, valid_len);
+#pragma unroll
+  for (int j = 0; j < N4; ++j) {
+    const int c = lane + 64 * j;
+    const float4_t gv = reinterpret_cast<const float4_t*>(gamma)[c];
+    const float4_t hv = reinterpret_cast<const float4_t*>(beta)[c];
+    float4_t n;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) n[e] = zero ? 0.f : (r[j][e] - mean) * rstd * gv[e] + hv[e];
+    reinterpret_cast<float4_t*>(ln_out)[row * C4 + c] = n;
+  }
+}
+
 unsigned grid_for(int64_t n4) {
   const int64_t blocks = (n4 + ET - 1) / ET;
   return (unsigned)(blocks < 256 * 32 ? blocks : 256 * 32);
@@ -87,5 +150,31 @@ extern "C" int tj_bias_gelu(float* y, const float* bias, int64_t rows, int64_t c
   if (!tjh::aligned16(y) || !tjh::aligned16(bias)) return TJ_ERR_ALIGN;
   const int64_t n4 = rows * (cols / 4);
   hipLaunchKernelGGL(tj::bias_gelu_kernel, dim3(tj::grid_for(n4)), dim3(tj::ET), 0, stream, y, bias, n4, cols / 4);
+  return tjh::launch_status();
+}
+
+extern "C" int tj_bias_residual_layernorm(float* out, float* ln_out, const float* x, const float* y,
+                                          const float* bias, const float* gamma, const float* beta, int64_t rows,
+                                          int64_t cols, int64_t seq_len, const int32_t* valid_len, int mode,
+                                          float eps, int zero_ln_padded, hipStream_t stream) {
+  if (rows < 0 || cols <= 0 || seq_len <= 0 || mode < 0 || mode > 2 || !(eps >= 0.f)) return TJ_ERR_SHAPE;
+  if ((mode != 0 || zero_ln_padded) && valid_len != nullptr && rows % seq_len != 0) return TJ_ERR_SHAPE;
+  if (cols % 256 != 0 || cols > 2048) return TJ_ERR_UNSUPPORTED;
+  if (rows == 0) return TJ_OK;
+  if (!out || !ln_out || !x || !y || !bias || !gamma || !beta) return TJ_ERR_SHAPE;
+  for (const void* p : {(const void*)out, (const void*)ln_out, (const void*)x, (const void*)y, (const void*)bias,
+                        (const void*)gamma, (const void*)beta})
+    if (!tjh::aligned16(p)) return TJ_ERR_ALIGN;
+  if ((int64_t)ln_out < (int64_t)out + rows * cols * 4 && (int64_t)out < (int64_t)ln_out + rows * cols * 4)
+    return TJ_ERR_SHAPE;  // the norm output must not overlap the residual stream
+  const dim3 grid((unsigned)((rows + tj::ET / 64 - 1) / (tj::ET / 64)));
+  const int32_t* vl = (mode == 0 && !zero_ln_padded) ? nullptr : valid_len;
+  switch (cols / 256) {
+    case 1: hipLaunchKernelGGL(tj::bias_residual_ln_kernel<1>, grid, dim3(tj::ET), 0, stream, out, ln_out, x, y, bias, gamma, beta, rows, seq_len, vl, mode, eps, zero_ln_padded); break;
+    case 2: hipLaunchKernelGGL(tj::bias_residual_ln_kernel<2>, grid, dim3(tj::ET), 0, stream, out, ln_out, x, y, bias, gamma, beta, rows, seq_len, vl, mode, eps, zero_ln_padded); break;
+    case 4: hipLaunchKernelGGL(tj::bias_residual_ln_kernel<4>, grid, dim3(tj::ET), 0, stream, out, ln_out, x, y, bias, gamma, beta, rows, seq_len, vl, mode, eps, zero_ln_padded); break;
+    case 8: hipLaunchKernelGGL(tj::bias_residual_ln_kernel<8>, grid, dim3(tj::ET), 0, stream, out, ln_out, x, y, bias, gamma, beta, rows, seq_len, vl, mode, eps, zero_ln_padded); break;
+    default: return TJ_ERR_UNSUPPORTED;
+  }
   return tjh::launch_status();
 }

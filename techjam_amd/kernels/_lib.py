@@ -60,6 +60,10 @@ SIGNATURES = {
     ),
     "tj_bias_residual": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _int, _vp]),
     "tj_bias_gelu": (_int, [_vp, _vp, _i64, _i64, _vp]),
+    "tj_bias_residual_layernorm": (
+        _int,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _int, _f32, _int, _vp],
+    ),
     "tj_quad_apply": (
         _int,
         [_vp, _vp, _vp, _int, _i64, _i64, _i64, _i64, _i64p, _i64p, _i64p, _vp],

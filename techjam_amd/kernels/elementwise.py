@@ -3,8 +3,10 @@
 ``bias_residual`` and ``bias_gelu`` replace the bias add / residual add /
 ``masked_fill`` and bias add / exact GELU pairs that follow the block's
 projection GEMMs (``torch_transformer_benchmark.py:116-121``, ``:140-145``)
-with one pass each. Both return ``None`` for layouts the kernels do not take
-(non-fp32, a last dimension that is not a multiple of 4, unaligned or
+with one pass each; ``bias_residual_layernorm`` also produces the LayerNorm of
+the residual stream that the next step reads. They return ``None`` for
+layouts the kernels do not take (non-fp32, a last dimension that is not a
+multiple of 4 -- of 256 up to 2048 for the norm --, unaligned or
 non-contiguous tensors), and the caller then uses the plain tensor ops.
 """
 
@@ -54,3 +56,32 @@ def bias_gelu(y: torch.Tensor, bias: torch.Tensor) -> Optional[torch.Tensor]:
                                    _stream_ptr(y.device))
     _lib.check(code, "tj_bias_gelu")
     return y
+
+
+def bias_residual_layernorm(x: torch.Tensor, y: torch.Tensor, bias: torch.Tensor,
+                            valid_len: Optional[torch.Tensor], mode: int, norm: torch.nn.LayerNorm,
+                            out: Optional[torch.Tensor] = None, zero_padded_norm: bool = False):
+    """``bias_residual`` and ``norm`` of its result in one pass: ``(out, norm(out))``.
+
+    With ``zero_padded_norm`` the norm output of padded rows is zero (the final
+    ``masked_fill``). ``None`` when the shapes or the norm are not covered.
+    """
+    c = x.shape[-1] if x.ndim == 3 else 0
+    if (x.ndim != 3 or y.shape != x.shape or bias.shape != (c,) or c % 256 or c > 2048 or (c // 256) & (c // 256 - 1)
+            or not isinstance(norm, torch.nn.LayerNorm) or tuple(norm.normalized_shape) != (c,)
+            or norm.weight is None or norm.bias is None):
+        return None
+    if valid_len is not None and (valid_len.dtype != torch.int32 or valid_len.shape != (x.shape[0],)
+                                  or valid_len.device != x.device):
+        return None
+    out = torch.empty_like(x) if out is None else out
+    ln = torch.empty_like(x)
+    if not _ok(x, y, bias, out, ln, norm.weight, norm.bias):
+        return None
+    b, s, _ = x.shape
+    code = _lib.lib().tj_bias_residual_layernorm(
+        out.data_ptr(), ln.data_ptr(), x.data_ptr(), y.data_ptr(), bias.data_ptr(), norm.weight.data_ptr(),
+        norm.bias.data_ptr(), b * s, c, s, None if valid_len is None else valid_len.data_ptr(), mode,
+        float(norm.eps), int(bool(zero_padded_norm)), _stream_ptr(x.device))
+    _lib.check(code, "tj_bias_residual_layernorm")
+    return out, ln

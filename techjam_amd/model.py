@@ -175,6 +175,24 @@ class EncoderBlock(nn.Module):
         y = F.linear(h, self.ffn_out.weight)
         return _must(bias_residual(x, y, self.ffn_out.bias, valid_len, MODE_ZERO_OUT, out=y))
 
+    def _forward_fused_norms(self, x, xn, valid_token_mask, causal, valid_len, next_norm, last):
+        """``_forward_fused`` that takes ``norm1(x)`` ready-made and hands back
+        ``(x_out, next_norm(x_out))``: each residual pass also writes the
+        LayerNorm its result feeds (``norm2`` here, then the next block's
+        ``norm1`` or the final norm, with padded rows zeroed after the last
+        block)."""
+        from .kernels.elementwise import MODE_ZERO_OUT, MODE_ZERO_Y, bias_gelu, bias_residual_layernorm
+
+        attn = self.attention
+        ctx = attn.context(xn, valid_token_mask, causal, valid_len)
+        y = F.linear(ctx, attn.out_proj.weight)
+        x, xn2 = _must(bias_residual_layernorm(x, y, attn.out_proj.bias, valid_len, MODE_ZERO_Y, self.norm2, out=y))
+        h = F.linear(xn2, self.ffn_in.weight)
+        _must(bias_gelu(h, self.ffn_in.bias))
+        y = F.linear(h, self.ffn_out.weight)
+        return _must(bias_residual_layernorm(x, y, self.ffn_out.bias, valid_len, MODE_ZERO_OUT, next_norm, out=y,
+                                             zero_padded_norm=last and valid_token_mask is not None))
+
 
 def _must(t):
     if t is None:
@@ -195,12 +213,33 @@ class TransformerEncoder(nn.Module):
         self.final_norm = nn.LayerNorm(config.d_model)
 
     def forward_layers(self, x, valid_token_mask=None, valid_len=None):
+        if self._can_fuse_norms(x, valid_token_mask, valid_len):
+            return self._forward_layers_fused(x, valid_token_mask, valid_len)
         for layer in self.layers:
             x = layer(x, valid_token_mask, self.config.causal, valid_len=valid_len)
         x = self.final_norm(x)
         if valid_token_mask is not None:
             x.masked_fill_(~valid_token_mask[..., None], 0)  # x is the norm's fresh output
         return x
+
+    def _can_fuse_norms(self, x, valid_token_mask, valid_len) -> bool:
+        d = x.shape[-1] if x.ndim == 3 else 0
+        norms = [m for layer in self.layers for m in (layer.norm1, layer.norm2)] + [self.final_norm]
+        return (len(self.layers) > 0 and d in (256, 512, 1024, 2048)
+                and all(layer._can_fuse(x, valid_token_mask, valid_len) for layer in self.layers)
+                and all(type(n) is nn.LayerNorm and n.elementwise_affine and n.bias is not None
+                        and n.weight.dtype == torch.float32 for n in norms))
+
+    def _forward_layers_fused(self, x, valid_token_mask, valid_len):
+        """The layer stack with every LayerNorm but the first fused into the
+        residual pass before it (same computation as the loop above)."""
+        xn = self.layers[0].norm1(x)
+        n = len(self.layers)
+        for i, layer in enumerate(self.layers):
+            nxt = self.layers[i + 1].norm1 if i + 1 < n else self.final_norm
+            x, xn = layer._forward_fused_norms(x, xn, valid_token_mask, self.config.causal, valid_len, nxt,
+                                               last=i + 1 == n)
+        return xn
 
     def forward(self, x, valid_token_mask: Optional[torch.Tensor] = None):
         valid_len = None if valid_token_mask is None else prefix_lengths(valid_token_mask)

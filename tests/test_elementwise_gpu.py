@@ -71,3 +71,43 @@ def test_unsupported_layouts_are_declined(cuda):
     x, y, bias, _, _ = _case(cuda)
     assert bias_residual(x.transpose(0, 1), y.transpose(0, 1), bias, None, MODE_PLAIN) is None
     assert bias_gelu(y.half(), bias.half()) is None                     # fp32 only
+
+
+@pytest.mark.parametrize("c", [256, 512, 1024, 2048])
+@pytest.mark.parametrize("masked", [False, True])
+def test_bias_residual_layernorm_matches_tensor_ops(cuda, c, masked):
+    """The residual pass is bitwise the tensor ops; the fused LayerNorm is
+    within fp32 rounding of torch's (two exact passes vs torch's reduction)."""
+    from techjam_amd.kernels.elementwise import MODE_ZERO_OUT, MODE_ZERO_Y, bias_residual_layernorm
+
+    x, y, bias, lens, mask = _case(cuda, c=c, seed=10 + c)
+    norm = torch.nn.LayerNorm(c).to(cuda)
+    with torch.no_grad():
+        norm.weight.normal_(1.0, 0.2)
+        norm.bias.normal_(0.0, 0.2)
+    vl = lens if masked else None
+    m = mask[..., None] if masked else torch.ones_like(mask)[..., None]
+    for mode, want in ((MODE_ZERO_Y, x + (y + bias).masked_fill(~m, 0)),
+                       (MODE_ZERO_OUT, (x + (y + bias)).masked_fill(~m, 0))):
+        for zero in (False, True):
+            out, ln = bias_residual_layernorm(x, y, bias, vl, mode, norm, zero_padded_norm=zero)
+            assert torch.equal(out, want)
+            want_ln = F.layer_norm(want, (c,), norm.weight, norm.bias, norm.eps)
+            if zero and masked:
+                want_ln = want_ln.masked_fill(~m, 0)
+            err = (ln - want_ln).abs().max().item()
+            assert err < 2e-5, f"mode {mode} zero {zero}: {err:.2e}"
+
+
+def test_bias_residual_layernorm_in_place_and_unsupported_widths(cuda):
+    from techjam_amd.kernels.elementwise import MODE_ZERO_OUT, bias_residual_layernorm
+
+    x, y, bias, lens, mask = _case(cuda, c=512, seed=21)
+    norm = torch.nn.LayerNorm(512).to(cuda)
+    want = (x + (y + bias)).masked_fill(~mask[..., None], 0)
+    out, ln = bias_residual_layernorm(x, y, bias, lens, MODE_ZERO_OUT, norm, out=y)
+    assert out.data_ptr() == y.data_ptr() and torch.equal(out, want)
+    assert (ln - F.layer_norm(want, (512,), norm.weight, norm.bias, norm.eps)).abs().max().item() < 2e-5
+    for c in (64, 768, 4096):  # not a power-of-two multiple of 256 up to 2048
+        x, y, bias, lens, _ = _case(cuda, c=c, seed=22)
+        assert bias_residual_layernorm(x, y, bias, lens, MODE_ZERO_OUT, torch.nn.LayerNorm(c).to(cuda)) is None
