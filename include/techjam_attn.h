@@ -102,8 +102,8 @@ int tj_attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype,
  * adds its bias (the packed projection of sdpa.py:127-138 through
  * torch.nn.Linear).
  *
- * q_bias, v_bias: device fp32 [H * D] (head h at h * D), 4-byte aligned, or
- * NULL. No row limits or split scores on this entry point.
+ * q_bias, v_bias: device fp32 [H * D] (head h at h * D), 16-byte aligned,
+ * or NULL. No row limits or split scores on this entry point.
  */
 int tj_attn_fwd_proj_bias(const void* q, const void* k, const void* v, void* o, int dtype,
                           int64_t B, int64_t H, int64_t S, int64_t D,

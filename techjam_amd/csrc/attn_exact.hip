@@ -215,14 +215,23 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
 #pragma unroll
       for (int ks = 0; ks < TL::KS; ++ks) {
         const int d0 = 16 * ks + 8 * hl;
+        // q bias of these eight dims (two 16-byte loads; zeros without one)
+        float bq[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (a.q_bias != nullptr) {
+#pragma unroll
+          for (int f = 0; f < 2; ++f) {
+            const float4_t t = *reinterpret_cast<const float4_t*>(a.q_bias + h * HD + d0 + 4 * f);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bq[4 * f + j] = t[j];
+          }
+        }
 #pragma unroll
         for (int e = 0; e < 8; e += Vec16<T>::N) {
           Vec16<T> x;
           if (in) x.load(qp + base + d0 + e); else x.zero();
 #pragma unroll
           for (int j = 0; j < Vec16<T>::N; ++j) {
-            const float bq = a.q_bias != nullptr ? a.q_bias[h * HD + d0 + e + j] : 0.f;
-            const float y = (x.get(j) + bq) * a.qscale;
+            const float y = (x.get(j) + bq[e + j]) * a.qscale;
             const half_t hi = (half_t)y;
             qf[qb][ks][e + j] = hi;
             if constexpr (SPLIT) qlo[qb][ks][e + j] = (half_t)(y - (float)hi);
@@ -375,9 +384,10 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int d0 = db * 32 + 8 * g + 4 * hl;
+          const float4_t bv = vb != nullptr ? *reinterpret_cast<const float4_t*>(vb + d0) : float4_t{0.f, 0.f, 0.f, 0.f};
           float y[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) y[e] = oacc[qb][db][4 * g + e] * inv + (vb != nullptr ? vb[d0 + e] : 0.f);
+          for (int e = 0; e < 4; ++e) y[e] = oacc[qb][db][4 * g + e] * inv + bv[e];
           if constexpr (sizeof(T) == 4) {
             *reinterpret_cast<float4_t*>(op + d0) = float4_t{y[0], y[1], y[2], y[3]};
           } else {
@@ -487,7 +497,7 @@ int attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype, in
   if (!tjh::view_ok(q, q_strides, dtype) || !tjh::view_ok(k, k_strides, dtype) ||
       !tjh::view_ok(v, v_strides, dtype) || !tjh::view_ok(o, o_strides, dtype))
     return TJ_ERR_ALIGN;
-  if ((reinterpret_cast<uintptr_t>(q_bias) | reinterpret_cast<uintptr_t>(v_bias)) & 3u) return TJ_ERR_ALIGN;
+  if ((reinterpret_cast<uintptr_t>(q_bias) | reinterpret_cast<uintptr_t>(v_bias)) & 15u) return TJ_ERR_ALIGN;
   // K and V rows of one (b, h) are addressed with 31-bit byte offsets.
   for (const int64_t* st : {k_strides, v_strides}) {
     if (st[2] < 0 || ((S - 1) * st[2] + D) * tjh::elem_size(dtype) >= (int64_t(1) << 31))

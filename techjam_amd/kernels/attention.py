@@ -138,8 +138,9 @@ def scaled_dot_product_attention(
             raise ValueError("q_bias / v_bias do not combine with row_limit or qk_split")
         for name, t in (("q_bias", q_bias), ("v_bias", v_bias)):
             if t is not None and (t.dtype != torch.float32 or t.device != dev or t.numel() != h * d
-                                  or not t.is_contiguous()):
-                raise ValueError(f"{name} must be a contiguous float32 tensor of {h * d} elements on {dev}")
+                                  or not t.is_contiguous() or t.data_ptr() % 16):
+                raise ValueError(f"{name} must be a contiguous, 16-byte aligned float32 tensor of {h * d} "
+                                 f"elements on {dev}")
         code = _lib.lib().tj_attn_fwd_proj_bias(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), _DTYPES[q.dtype],
             b, h, s, d,

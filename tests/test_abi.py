@@ -66,9 +66,9 @@ def test_attn_proj_bias_rejects_bad_arguments_before_launching():
     f = L.tj_attn_fwd_proj_bias
     assert f(*args, 7, 1, 4, 128, 64, st, st, st, st, 0.125, 1, None, 16, 16, None) == _lib.TJ_ERR_DTYPE
     assert f(*args, _lib.TJ_F32, 1, 4, 128, 48, st, st, st, st, 0.125, 1, None, 16, 16, None) == _lib.TJ_ERR_UNSUPPORTED
-    # bias pointers must be 4-byte aligned
-    assert f(*args, _lib.TJ_F32, 1, 4, 128, 64, st, st, st, st, 0.125, 1, None, 18, 16, None) == _lib.TJ_ERR_ALIGN
-    assert f(*args, _lib.TJ_F32, 1, 4, 128, 64, st, st, st, st, 0.125, 1, None, 16, 17, None) == _lib.TJ_ERR_ALIGN
+    # bias pointers must be 16-byte aligned
+    assert f(*args, _lib.TJ_F32, 1, 4, 128, 64, st, st, st, st, 0.125, 1, None, 20, 16, None) == _lib.TJ_ERR_ALIGN
+    assert f(*args, _lib.TJ_F32, 1, 4, 128, 64, st, st, st, st, 0.125, 1, None, 16, 24, None) == _lib.TJ_ERR_ALIGN
     assert f(*args, _lib.TJ_F32, 0, 4, 128, 64, st, st, st, st, 0.125, 1, None, 16, 16, None) == _lib.TJ_OK
 
 
