@@ -165,11 +165,29 @@ struct KVStage {
           }
         }
         const int slot = key_slot(4 * g);
+        if constexpr (sizeof(T) == 2) {
+          // fp16 rows: dword m of the four key rows holds elements 2m, 2m+1;
+          // byte permutes gather them column-wise (element-wise extraction
+          // from a 16-byte register goes through scratch memory).
+          using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
+          using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
 #pragma unroll
-        for (int e = 0; e < TL::VEC; ++e) {
-          half4_t hv = {(half_t)vx[p][0].get(e), (half_t)vx[p][1].get(e),
-                        (half_t)vx[p][2].get(e), (half_t)vx[p][3].get(e)};
-          *reinterpret_cast<half4_t*>(&sm.vt[buf][c * TL::VEC + e][slot]) = hv;
+          for (int m = 0; m < TL::VEC / 2; ++m) {
+            uint32_t d[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) d[r] = __builtin_bit_cast(u32x4, vx[p][r].v)[m];
+            const u32x2 lo = {__builtin_amdgcn_perm(d[1], d[0], 0x05040100u), __builtin_amdgcn_perm(d[3], d[2], 0x05040100u)};
+            const u32x2 hi = {__builtin_amdgcn_perm(d[1], d[0], 0x07060302u), __builtin_amdgcn_perm(d[3], d[2], 0x07060302u)};
+            *reinterpret_cast<half4_t*>(&sm.vt[buf][c * TL::VEC + 2 * m][slot]) = __builtin_bit_cast(half4_t, lo);
+            *reinterpret_cast<half4_t*>(&sm.vt[buf][c * TL::VEC + 2 * m + 1][slot]) = __builtin_bit_cast(half4_t, hi);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < TL::VEC; ++e) {
+            half4_t hv = {(half_t)vx[p][0].get(e), (half_t)vx[p][1].get(e),
+                          (half_t)vx[p][2].get(e), (half_t)vx[p][3].get(e)};
+            *reinterpret_cast<half4_t*>(&sm.vt[buf][c * TL::VEC + e][slot]) = hv;
+          }
         }
       }
     }

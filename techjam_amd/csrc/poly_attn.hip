@@ -118,8 +118,11 @@ __device__ __forceinline__ void load_row4(const T* p, float out[4]) {
 // on the loads before the tile is stored: k is scaled by rs at the store.
 template <typename T>
 struct TokTile {
-  float kx[4][4];
-  float vx[4][4];
+  // Raw rows as loaded (fp32 or fp16), converted at the stores: fp16 input
+  // holds half the registers.
+  using Raw = std::conditional_t<sizeof(T) == 4, float4_t, half4_t>;
+  Raw kx[4];
+  Raw vx[4];
   __amdgpu_buffer_rsrc_t rk, rv;
   uint32_t koff, voff, kstep, vstep;
   __device__ __forceinline__ static void coords(int tid, int& g, int& c) {
@@ -146,13 +149,13 @@ struct TokTile {
       if constexpr (sizeof(T) == 4) {
         const float4_t x = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rk, koff, (tok0 + r) * kstep, 0));
         const float4_t y = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rv, voff, (tok0 + r) * vstep, 0));
-#pragma unroll
-        for (int e = 0; e < 4; ++e) { kx[r][e] = x[e]; vx[r][e] = y[e]; }
+        kx[r] = x;
+        vx[r] = y;
       } else {
         const half4_t x = __builtin_bit_cast(half4_t, __builtin_amdgcn_raw_buffer_load_b64(rk, koff, (tok0 + r) * kstep, 0));
         const half4_t y = __builtin_bit_cast(half4_t, __builtin_amdgcn_raw_buffer_load_b64(rv, voff, (tok0 + r) * vstep, 0));
-#pragma unroll
-        for (int e = 0; e < 4; ++e) { kx[r][e] = (float)x[e]; vx[r][e] = (float)y[e]; }
+        kx[r] = x;
+        vx[r] = y;
       }
     }
   }
@@ -168,7 +171,8 @@ struct TokTile {
       const int d = 4 * c + e;
       const int off = d * 128 + 16 * ((g >> 1) ^ ((d >> 1) & 7)) + 8 * (g & 1);
       *reinterpret_cast<half4_t*>(dst + off) =
-          half4_t{(half_t)(kx[0][e] * rs), (half_t)(kx[1][e] * rs), (half_t)(kx[2][e] * rs), (half_t)(kx[3][e] * rs)};
+          half4_t{(half_t)((float)kx[0][e] * rs), (half_t)((float)kx[1][e] * rs), (half_t)((float)kx[2][e] * rs),
+                  (half_t)((float)kx[3][e] * rs)};
       *reinterpret_cast<half4_t*>(dst + PD * 128 + off) =
           half4_t{(half_t)vx[0][e], (half_t)vx[1][e], (half_t)vx[2][e], (half_t)vx[3][e]};
     }
@@ -179,7 +183,8 @@ struct TokTile {
     coords(tid, g, c);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      half4_t hk = {(half_t)(kx[r][0] * rs), (half_t)(kx[r][1] * rs), (half_t)(kx[r][2] * rs), (half_t)(kx[r][3] * rs)};
+      half4_t hk = {(half_t)((float)kx[r][0] * rs), (half_t)((float)kx[r][1] * rs), (half_t)((float)kx[r][2] * rs),
+                    (half_t)((float)kx[r][3] * rs)};
       *reinterpret_cast<half4_t*>(&kb[4 * g + r][4 * c]) = hk;
     }
     const int slot = key_slot(4 * g);
