@@ -115,6 +115,21 @@ def test_config_4_long_sequence_on_the_linear_memory_oracle(cuda):
     _check(cfg, (1234,), 0.5, cuda, oracle_on_gpu=True, oracle_cls=LinearMemoryReference)
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_unmasked_encoder_forward(cuda, causal):
+    """No mask at all: the fused tails and norms run with every row valid."""
+    cfg = OracleConfig(2, 300, 512, 8, 1024, 2, causal)
+    base, cand = _pair(cfg, 77, cuda)
+    x = torch.randn(2, 300, 512, generator=torch.Generator().manual_seed(5))
+    with torch.inference_mode():
+        with _matmul_flags("highest", False):
+            ref = base(x, None)
+            got = cand(x.to(cuda), None)
+            torch.cuda.synchronize()
+    res = compare_outputs(ref, got.cpu(), rtol=0.02, atol=0.002)
+    assert res.passed, f"{res.failed_elements} failed, max_abs {res.max_abs_error:.3e}"
+
+
 def test_padded_rows_are_zero_and_route_is_cached(cuda):
     cfg = OracleConfig(2, 128, 256, 4, 1024, 1, True)
     _, cand = _pair(cfg, 1, cuda)
