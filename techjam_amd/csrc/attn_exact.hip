@@ -22,9 +22,15 @@
 //     the right-padding key mask is redundant (every valid row i only sees
 //     keys j <= i < L) and is not applied; padded rows i >= L are written as 0.
 //   * Grid: tile ids are remapped so that all query tiles of one (b, h) land on
-//     one XCD (K/V stay in that XCD's L2), heaviest (last) query tile first.
-//     Launches with row limits, whose work sits on a few (b, h), instead
-//     spread every (b, h) over all XCDs.
+//     one XCD. Each XCD takes a contiguous range of (b, h). A long range is
+//     walked one (b, h) at a time, heaviest (last) query tile first, so the
+//     tiles of a (b, h) start close together and share its K/V sweep in L2;
+//     its last group of (b, h) (about one XCD's worth of workgroup slots) is
+//     interleaved instead, heaviest tiles first across the group, so that no
+//     heavy tile starts late and the XCD's tail stays short. A short range
+//     (at most two such groups) is interleaved group by group throughout.
+//     Launches with row limits, whose work sits on a few (b, h), and launches
+//     with fewer than eight (b, h) spread every (b, h) over all XCDs.
 //   * Heads flagged in qk_split compute QK^T from a two-term fp16 expansion of
 //     q and k (x = hi + lo, both fp16) with three MFMAs -- hi.hi + hi.lo +
 //     lo.hi -- which restores fp32-level score accuracy where the score range
@@ -55,9 +61,8 @@ struct AttnArgs {
   const float* q_bias;  // [H * D] fp32 or null: added to q before scaling
   const float* v_bias;  // [H * D] fp32 or null: added to every valid output row
   int n_mtiles;
-  int total_tiles;
-  int per_xcd;
-  int balanced;  // row_limit launches: spread every (b, h) over all XCDs
+  int group;     // (b, h) per interleaved group on one XCD
+  int balanced;  // spread every (b, h) over all XCDs (row limits or B*H < 8)
 };
 
 template <typename T, int HD>
@@ -420,8 +425,7 @@ template <typename T, int HD, int QB, bool SPLIT_OK>
 __global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnArgs a) {
   __shared__ Smem<HD, SPLIT_OK> sm;
 
-  // XCD-aware tile order: ids x, x+8, x+16, ... run on XCD x and take
-  // consecutive logical tiles, i.e. all query tiles of a few (b, h).
+  // XCD-aware tile order: ids x, x+8, x+16, ... run on XCD x.
   const int id = blockIdx.x;
   int bh, mt;
   if (a.balanced) {
@@ -435,10 +439,31 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnArgs a) {
     bh = (id % bhn + mrev) % bhn;
     mt = a.n_mtiles - 1 - mrev;
   } else {
-    const int logical = (id % kNumXcd) * a.per_xcd + id / kNumXcd;
-    if (logical >= a.total_tiles) return;
-    bh = logical / a.n_mtiles;
-    mt = a.n_mtiles - 1 - logical % a.n_mtiles;
+    // XCD x owns (b, h) bh0 .. bh0 + nb - 1 (range sizes differ by at most
+    // one): the first nseq one after another, the rest in interleaved
+    // groups of a.group.
+    const int bhn = a.B * a.H;
+    const int x = id % kNumXcd;
+    const int j = id / kNumXcd;
+    const int bh0 = x * bhn / kNumXcd;
+    const int nb = (x + 1) * bhn / kNumXcd - bh0;
+    const int nseq = nb > 2 * a.group ? nb - a.group : 0;
+    int mrev;
+    if (j < nseq * a.n_mtiles) {
+      bh = bh0 + j / a.n_mtiles;
+      mrev = j % a.n_mtiles;
+    } else {
+      const int r = j - nseq * a.n_mtiles;
+      const int per_group = a.group * a.n_mtiles;
+      const int g0 = nseq + r / per_group * a.group;
+      if (g0 >= nb) return;
+      const int rr = r % per_group;
+      const int gs = min(a.group, nb - g0);
+      mrev = rr / gs;
+      if (mrev >= a.n_mtiles) return;
+      bh = bh0 + g0 + rr % gs;
+    }
+    mt = a.n_mtiles - 1 - mrev;
   }
   const int b = bh / a.H;
   const int h = bh % a.H;
@@ -461,17 +486,20 @@ __global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnArgs a) {
 template <typename T, int HD, int QB>
 int launch_qb(AttnArgs a, hipStream_t stream) {
   a.n_mtiles = (a.S + 128 * QB - 1) / (128 * QB);
-  a.total_tiles = a.B * a.H * a.n_mtiles;
-  a.per_xcd = (a.total_tiles + kNumXcd - 1) / kNumXcd;
-  a.balanced = a.row_limit != nullptr;
-  const int grid = a.balanced ? a.total_tiles : a.per_xcd * kNumXcd;
+  const int64_t bhn = int64_t(a.B) * a.H;
+  a.balanced = a.row_limit != nullptr || bhn < kNumXcd;
+  // About one XCD's worth of workgroup slots per group: 32 CUs x 2.
+  a.group = max(1, 64 / a.n_mtiles);
+  const int64_t per_xcd = (bhn + kNumXcd - 1) / kNumXcd;
+  const int64_t grid = a.balanced ? bhn * a.n_mtiles : kNumXcd * (per_xcd + a.group - 1) * a.n_mtiles;
+  if (grid * NT >= (int64_t(1) << 32)) return TJ_ERR_SHAPE;
   if constexpr (QB == 1) {
     if (a.qk_split != nullptr) {
-      hipLaunchKernelGGL((attn_fwd_kernel<T, HD, QB, true>), dim3(grid), dim3(NT), 0, stream, a);
+      hipLaunchKernelGGL((attn_fwd_kernel<T, HD, QB, true>), dim3(uint32_t(grid)), dim3(NT), 0, stream, a);
       return tjh::launch_status();
     }
   }
-  hipLaunchKernelGGL((attn_fwd_kernel<T, HD, QB, false>), dim3(grid), dim3(NT), 0, stream, a);
+  hipLaunchKernelGGL((attn_fwd_kernel<T, HD, QB, false>), dim3(uint32_t(grid)), dim3(NT), 0, stream, a);
   return tjh::launch_status();
 }
 
@@ -508,6 +536,8 @@ int attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype, in
              hipStream_t stream) {
   if (dtype != TJ_F32 && dtype != TJ_F16) return TJ_ERR_DTYPE;
   if (B < 0 || H <= 0 || S < 0 || D <= 0) return TJ_ERR_SHAPE;
+  // Tile indices fit 31 bits; the launch also checks that its grid fits the
+  // 32-bit dispatch size.
   if (B * H * ((S + 127) / 128) >= (int64_t(1) << 31) || S >= (int64_t(1) << 30)) return TJ_ERR_SHAPE;
   if (D != 32 && D != 64 && D != 128) return TJ_ERR_UNSUPPORTED;
   if (B == 0 || S == 0) return TJ_OK;

@@ -84,6 +84,8 @@ def test_attn_rejects_bad_arguments_before_launching():
     assert L.tj_attn_fwd(*args, _lib.TJ_F32, 1, 4, 128, 48, st, st, st, st, 0.125, 1, None, None, None, None) == _lib.TJ_ERR_UNSUPPORTED
     # negative sizes
     assert L.tj_attn_fwd(*args, _lib.TJ_F32, -1, 4, 128, 64, st, st, st, st, 0.125, 1, None, None, None, None) == _lib.TJ_ERR_SHAPE
+    # grids beyond the 32-bit dispatch size: 2**20 (b, h) x 128 tiles x 256 threads >= 2**32
+    assert L.tj_attn_fwd(*args, _lib.TJ_F16, 65536, 16, 32768, 32, st, st, st, st, 0.125, 1, None, None, None, None) == _lib.TJ_ERR_SHAPE
     # innermost stride != 1
     bad = _strides(64 * 128 * 4, 64, 64 * 4, 2)
     assert L.tj_attn_fwd(*args, _lib.TJ_F32, 1, 4, 128, 64, bad, st, st, st, 0.125, 1, None, None, None, None) == _lib.TJ_ERR_ALIGN
