@@ -14,6 +14,11 @@ Prints ONE JSON line with the driver's fields plus
   cpu_baseline : the dense FP32 oracle on this host's cores over a bounded
                  sample of the same workload (one batch element).
 
+Also in the line: ``environment`` (host, software, device), ``gpu_state``
+(rocm-smi clocks/power/temperature sampled after the timed region) and, with
+``--aa-reps N``, ``noise``: the step timed against itself N times, interleaved,
+giving the A/A floor below which two measurements are not distinguishable.
+
 Other workloads (``--workload``) exist for manual measurement; the driver
 runs the default.
 """
@@ -34,6 +39,9 @@ import torch
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
+from techjam_amd.infra.environment import collect_environment, collect_gpu_state  # noqa: E402
+from techjam_amd.infra.timing import summarise_timings, time_interleaved  # noqa: E402
+
 PEAK_MFMA_F16_TFLOPS = 2500.0   # MI355X dense fp16/bf16
 PEAK_HBM_GBS = 8000.0           # MI355X HBM3E
 
@@ -50,6 +58,9 @@ def parse_args():
                             "quad-apply", "quad-update", "causal-diag"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-repeats", type=int, default=3)
+    p.add_argument("--aa-reps", type=int, default=0,
+                   help="after the timed region, time the step against itself (A/A control, "
+                        "interleaved) this many times and report the noise floor")
     # Float32 GEMM flags of the model workloads; the defaults are the reference
     # harness's validated contract (src/benchmark.py:133-141, src/dispatcher.py:69-70).
     p.add_argument("--matmul-precision", choices=("highest", "high", "medium"), default="high")
@@ -276,6 +287,12 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = e0.elapsed_time(e1) / args.steps
+    gpu_state = collect_gpu_state(dev)
+    noise = None
+    if args.aa_reps > 0:
+        samples = time_interleaved({"step_ms": step, "step_control_ms": step}, args.aa_reps)
+        stats = summarise_timings(samples, [("step_ms", "step_control_ms")])
+        noise = {"samples_ms": samples, "variants": stats["variants"], **stats["noise"]}
 
     sec = ms_per_step / 1e3
     tflops = flops / sec / 1e12
@@ -320,7 +337,11 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "wall_s_timed_region": round(wall, 4),
+        "environment": collect_environment(torch, dev),
+        "gpu_state": gpu_state,
     }
+    if noise is not None:
+        line["noise"] = noise
     print(json.dumps(line), flush=True)
     return 0
 
