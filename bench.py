@@ -65,6 +65,8 @@ def parse_args():
     # harness's validated contract (src/benchmark.py:133-141, src/dispatcher.py:69-70).
     p.add_argument("--matmul-precision", choices=("highest", "high", "medium"), default="high")
     p.add_argument("--allow-tf32", action=argparse.BooleanOptionalAction, default=True)
+    # Opt-in: encoder GEMM operands rounded to fp16 (TF32's mantissa), fp32 accumulation.
+    p.add_argument("--gemm-operands", choices=("fp32", "fp16"), default="fp32")
     return p.parse_args()
 
 
@@ -200,6 +202,7 @@ def model(name):
         cand = DispatchingTransformer(cfg).eval()
         cand.load_state_dict(base.state_dict())
         cand = cand.to(dev)
+        cand.gemm_operands = args.gemm_operands
         x, mask = generate_random_case(cfg, torch.device("cpu"), torch.float32, 1234 + 100000,
                                        c.padding_ratio, 1.0)
         x, mask = x.to(dev), mask.to(dev)
@@ -218,7 +221,9 @@ def model(name):
                   "heads": c.num_heads, "ffn_dim": c.ffn_dim, "layers": c.num_layers,
                   "roofline_scope": "attention FLOPs over the whole forward (GEMMs not counted)",
                   "gemm": f"hipBLASLt, fp32 tensors, matmul precision {args.matmul_precision!r}, "
-                          f"allow_tf32={args.allow_tf32}"}
+                          f"allow_tf32={args.allow_tf32}"
+                          if args.gemm_operands == "fp32" else
+                          "hipBLASLt, fp16-rounded operands (TF32 mantissa), fp32 accumulation"}
         return step, c.batch_size * c.seq_len, flops, 0.0, config, f"model_{name.lower()}.md"
     return build
 

@@ -23,10 +23,9 @@ from __future__ import annotations
 from typing import Optional
 
 import torch
-import torch.nn.functional as F
 
 from ..kernels.attention import scaled_dot_product_attention
-from ..model import HipSelfAttention, linear
+from ..model import HipSelfAttention, linear, project
 
 
 class StridedSDPASelfAttention(HipSelfAttention):
@@ -90,10 +89,11 @@ class PackedQKVSDPASelfAttention(StridedSDPASelfAttention):
         return q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
 
     def project_qkv_folded(self, x: torch.Tensor):
-        """One bias-free ``[3D, D]`` GEMM; the q and v thirds of the packed bias
-        go to the kernel (the key third never changes the output)."""
+        """One bias-free ``[3D, D]`` GEMM (fp16 operands and result for an fp16
+        ``x``); the q and v thirds of the packed bias go to the kernel (the key
+        third never changes the output)."""
         b, s, _ = x.shape
-        packed = F.linear(x, self._packed_qkv_weight)
+        packed = project(x, self._packed_qkv_weight, self, "packed_qkv")
         q, k, v = packed.view(b, s, 3, self.num_heads, self.head_dim).unbind(dim=2)
         d = self.d_model
         return (q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),

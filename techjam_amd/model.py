@@ -62,6 +62,32 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor]) 
     return y
 
 
+def fp16_weight(owner: nn.Module, key: str, weight: torch.Tensor) -> torch.Tensor:
+    """Rounded fp16 copy of ``weight``, cached on ``owner`` and rebuilt
+    whenever the weight is replaced or modified in place."""
+    cache = owner.__dict__.setdefault("_fp16_weights", {})
+    tag = (weight.data_ptr(), weight._version, weight.device, tuple(weight.shape))
+    hit = cache.get(key)
+    if hit is None or hit[0] != tag:
+        hit = (tag, weight.detach().to(torch.float16))
+        cache[key] = hit
+    return hit[1]
+
+
+def project(x: torch.Tensor, weight: torch.Tensor, owner: nn.Module, key: str,
+            out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """Bias-free ``x @ weight.T``. A float32 ``x`` runs the float32 GEMM; a
+    float16 ``x`` runs on fp16 operands (the weight's cached fp16 copy) with
+    fp32 accumulation, its result in ``out_dtype`` (default float16)."""
+    if x.dtype != torch.float16:
+        return F.linear(x, weight)
+    w16 = fp16_weight(owner, key, weight)
+    if out_dtype in (None, torch.float16):
+        return F.linear(x, w16)
+    flat = x.reshape(-1, x.shape[-1])
+    return torch.mm(flat, w16.t(), out_dtype=out_dtype).view(*x.shape[:-1], w16.shape[0])
+
+
 class Linear(nn.Linear):
     """``nn.Linear`` with the same parameters and state-dict names whose
     forward is :func:`linear`."""
@@ -106,10 +132,12 @@ class HipSelfAttention(nn.Module):
                 and self.v_proj.bias is not None and self.q_proj.bias.dtype == torch.float32)
 
     def project_qkv_folded(self, x: torch.Tensor):
-        """Bias-free q, k, v head views and the q / v biases the kernel adds
-        (a key bias never changes the attention output)."""
-        return (self.heads_view(F.linear(x, self.q_proj.weight)), self.heads_view(F.linear(x, self.k_proj.weight)),
-                self.heads_view(F.linear(x, self.v_proj.weight)), self.q_proj.bias, self.v_proj.bias)
+        """Bias-free q, k, v head views (fp16 for an fp16 ``x``) and the q / v
+        biases the kernel adds (a key bias never changes the attention output)."""
+        return (self.heads_view(project(x, self.q_proj.weight, self.q_proj, "weight")),
+                self.heads_view(project(x, self.k_proj.weight, self.k_proj, "weight")),
+                self.heads_view(project(x, self.v_proj.weight, self.v_proj, "weight")),
+                self.q_proj.bias, self.v_proj.bias)
 
     def attend(self, q, k, v, valid_len, causal):
         return scaled_dot_product_attention(q, k, v, is_causal=causal, scale=self.scale, valid_len=valid_len)
@@ -175,21 +203,30 @@ class EncoderBlock(nn.Module):
         y = F.linear(h, self.ffn_out.weight)
         return _must(bias_residual(x, y, self.ffn_out.bias, valid_len, MODE_ZERO_OUT, out=y))
 
-    def _forward_fused_norms(self, x, xn, valid_token_mask, causal, valid_len, next_norm, last):
+    def _forward_fused_norms(self, x, xn, valid_token_mask, causal, valid_len, next_norm, last,
+                             fp16_operands=False):
         """``_forward_fused`` that takes ``norm1(x)`` ready-made and hands back
         ``(x_out, next_norm(x_out))``: each residual pass also writes the
         LayerNorm its result feeds (``norm2`` here, then the next block's
         ``norm1`` or the final norm, with padded rows zeroed after the last
-        block)."""
+        block).
+
+        ``fp16_operands`` rounds every GEMM input (normed activations, the
+        attention output, the GELU output, weights) to fp16 -- the 10-bit
+        mantissa of TF32 -- and accumulates in fp32; q, k, v leave their GEMM
+        as fp16 (the attention kernel rounds them to fp16 anyway), the other
+        GEMM results stay fp32, and so do the residual stream, LayerNorms,
+        softmax and GELU."""
         from .kernels.elementwise import MODE_ZERO_OUT, MODE_ZERO_Y, bias_gelu, bias_residual_layernorm
 
         attn = self.attention
-        ctx = attn.context(xn, valid_token_mask, causal, valid_len)
-        y = F.linear(ctx, attn.out_proj.weight)
+        f32 = torch.float32
+        ctx = attn.context(xn.half() if fp16_operands else xn, valid_token_mask, causal, valid_len)
+        y = project(ctx, attn.out_proj.weight, attn.out_proj, "weight", f32)
         x, xn2 = _must(bias_residual_layernorm(x, y, attn.out_proj.bias, valid_len, MODE_ZERO_Y, self.norm2, out=y))
-        h = F.linear(xn2, self.ffn_in.weight)
+        h = project(xn2.half() if fp16_operands else xn2, self.ffn_in.weight, self.ffn_in, "weight", f32)
         _must(bias_gelu(h, self.ffn_in.bias))
-        y = F.linear(h, self.ffn_out.weight)
+        y = project(h.half() if fp16_operands else h, self.ffn_out.weight, self.ffn_out, "weight", f32)
         return _must(bias_residual_layernorm(x, y, self.ffn_out.bias, valid_len, MODE_ZERO_OUT, next_norm, out=y,
                                              zero_padded_norm=last and valid_token_mask is not None))
 
@@ -203,6 +240,11 @@ def _must(t):
 class TransformerEncoder(nn.Module):
     """Layer stack plus final LayerNorm (``torch_transformer_benchmark.py:148-172``)."""
 
+    #: "fp32" (default): float32 GEMMs under torch's matmul precision setting.
+    #: "fp16": GEMM operands rounded to fp16 with fp32 accumulation (the
+    #: mantissa of TF32); fused GPU path only, other paths raise.
+    gemm_operands = "fp32"
+
     def __init__(self, config: TransformerConfig) -> None:
         super().__init__()
         self.config = config
@@ -213,8 +255,14 @@ class TransformerEncoder(nn.Module):
         self.final_norm = nn.LayerNorm(config.d_model)
 
     def forward_layers(self, x, valid_token_mask=None, valid_len=None):
+        if self.gemm_operands not in ("fp32", "fp16"):
+            raise ValueError(f"gemm_operands must be 'fp32' or 'fp16', not {self.gemm_operands!r}")
         if self._can_fuse_norms(x, valid_token_mask, valid_len):
             return self._forward_layers_fused(x, valid_token_mask, valid_len)
+        if self.gemm_operands == "fp16":
+            from .errors import UnsupportedCaseError
+
+            raise UnsupportedCaseError("fp16 GEMM operands are implemented on the fused GPU path only")
         for layer in self.layers:
             x = layer(x, valid_token_mask, self.config.causal, valid_len=valid_len)
         x = self.final_norm(x)
@@ -238,7 +286,7 @@ class TransformerEncoder(nn.Module):
         for i, layer in enumerate(self.layers):
             nxt = self.layers[i + 1].norm1 if i + 1 < n else self.final_norm
             x, xn = layer._forward_fused_norms(x, xn, valid_token_mask, self.config.causal, valid_len, nxt,
-                                               last=i + 1 == n)
+                                               last=i + 1 == n, fp16_operands=self.gemm_operands == "fp16")
         return xn
 
     def forward(self, x, valid_token_mask: Optional[torch.Tensor] = None):

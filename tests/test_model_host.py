@@ -1,0 +1,39 @@
+"""Host-side helpers of the encoder model (no GPU): the fp16 weight cache and
+the GEMM dispatch on the input's dtype."""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from techjam_amd.model import fp16_weight, project
+
+
+def test_fp16_weight_cache_follows_the_weight():
+    lin = torch.nn.Linear(8, 4)
+    w16 = fp16_weight(lin, "weight", lin.weight)
+    assert w16.dtype == torch.float16 and torch.equal(w16, lin.weight.detach().half())
+    assert fp16_weight(lin, "weight", lin.weight) is w16            # cached
+    with torch.no_grad():
+        lin.weight.mul_(2.0)                                         # in place: new version
+    w16b = fp16_weight(lin, "weight", lin.weight)
+    assert w16b is not w16 and torch.equal(w16b, lin.weight.detach().half())
+    lin.weight = torch.nn.Parameter(torch.ones(4, 8))                # replaced
+    assert torch.equal(fp16_weight(lin, "weight", lin.weight), torch.ones(4, 8, dtype=torch.float16))
+    assert fp16_weight(lin, "other", lin.bias).shape == (4,)          # keys are separate entries
+
+
+def test_project_keeps_fp32_inputs_on_the_fp32_gemm():
+    lin = torch.nn.Linear(8, 4, bias=False)
+    x = torch.randn(2, 3, 8)
+    assert torch.equal(project(x, lin.weight, lin, "weight"), F.linear(x, lin.weight))
+    assert "_fp16_weights" not in lin.__dict__
+
+
+def test_project_rounds_operands_for_fp16_inputs():
+    lin = torch.nn.Linear(8, 4, bias=False)
+    x = torch.randn(2, 3, 8)
+    y = project(x.half(), lin.weight, lin, "weight")
+    assert y.dtype == torch.float16 and y.shape == (2, 3, 4)
+    ref = x.half().double() @ lin.weight.detach().half().double().t()
+    assert torch.allclose(y.double(), ref, atol=2e-3, rtol=2e-3)
