@@ -1,6 +1,6 @@
 """CPU restatement of the reference's attention hot path -- TEST INFRASTRUCTURE.
 
-This package is the checker, never the product. Only ``tests/``,
+This package checks the product and is never part of it. Only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
 import it. The ``techjam_amd`` package must not import anything from here; its
 attention always runs the HIP kernels and fails loudly when they are missing.
