@@ -505,11 +505,14 @@ int launch_qb(AttnArgs a, hipStream_t stream) {
 
 // Two query blocks per wave halve LDS operand traffic per MFMA. They fit the
 // register budget only for head_dim <= 64 without split scores, and need
-// sequences long enough to fill 256-row tiles.
+// sequences long enough to fill 256-row tiles. Launches with fewer than 1024
+// such tiles (two per CU) keep 128-row tiles: there the heaviest tile sets
+// the time, and a 32-row block per wave halves its per-key-tile work.
 template <typename T, int HD>
 int launch(const AttnArgs& a, hipStream_t stream) {
   if constexpr (HD <= 64) {
-    if (a.S >= 512 && a.qk_split == nullptr) return launch_qb<T, HD, 2>(a, stream);
+    const int64_t wide_tiles = int64_t(a.B) * a.H * ((a.S + 255) / 256);
+    if (a.S >= 512 && a.qk_split == nullptr && wide_tiles >= 1024) return launch_qb<T, HD, 2>(a, stream);
   }
   return launch_qb<T, HD, 1>(a, stream);
 }
