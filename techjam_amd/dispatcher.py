@@ -28,6 +28,7 @@ Keeps the public interface of the reference's ``src/dispatcher.py:39-818`` --
 
 from __future__ import annotations
 
+import os
 import weakref
 from dataclasses import dataclass
 from typing import Callable, Dict, Optional, Tuple, Union
@@ -46,6 +47,7 @@ from .implementations.extreme import (
 from .implementations.sdpa import PackedQKVSDPASelfAttention, StridedSDPASelfAttention
 from .infra import BENCHMARK_CONFIGS, CandidateSpec, OfficialCase, load_official_cases
 from .kernels.attention import SUPPORTED_HEAD_DIMS
+from .graphs import GraphedForward, graph_key, weights_signature
 from .model import TransformerConfig, TransformerEncoder, config_key
 
 ConfigKey = Tuple[int, int, int, int, int, bool, int]
@@ -77,6 +79,11 @@ BENCHMARK_CASE_BY_CONFIG: Dict[ConfigKey, str] = {
 }
 PACKED_QKV_CASES = frozenset((2, 3, "C2", "C4"))
 EXTREME_CASES = (6, 14)
+# Launch-bound sizes replayed as HIP graphs (C1: 256 tokens; C2's 8192 and
+# C4's 16384 tokens are kernel-bound and gain nothing), and captures kept per
+# model.
+GRAPH_MAX_TOKENS = 4096
+GRAPH_CACHE_SIZE = 8
 
 
 def case_for(config) -> Optional[CaseId]:
@@ -167,6 +174,11 @@ def _device_arch(device: torch.device) -> Optional[str]:
 class DispatchingTransformer(TransformerEncoder):
     """Lazy per-instance dispatcher whose attention always runs the HIP kernels."""
 
+    #: Replay the exact-attention forward as a HIP graph for inputs of at most
+    #: ``GRAPH_MAX_TOKENS`` tokens (inference only); ``TECHJAM_AMD_GRAPHS=0``
+    #: in the environment turns it off.
+    use_graphs = True
+
     def __init__(self, config: TransformerConfig) -> None:
         super().__init__(config)
         case_id = case_for(config)
@@ -187,6 +199,8 @@ class DispatchingTransformer(TransformerEncoder):
         self._mask_version = None
         self._mask_kind: Optional[MaskKind] = None
         self._mask_lengths: Optional[torch.Tensor] = None
+        self._graphs: Dict[tuple, GraphedForward] = {}
+        self._graph_failures: Dict[tuple, str] = {}
 
     # -- diagnostics -------------------------------------------------------
     @property
@@ -203,6 +217,8 @@ class DispatchingTransformer(TransformerEncoder):
         return self._last_extreme_chunk_size
 
     def clear_runtime_cache(self) -> None:
+        self._graphs.clear()
+        self._graph_failures.clear()
         self._compiled_forwards.clear()
         self._compile_failures.clear()
         self._device_contracts.clear()
@@ -255,7 +271,37 @@ class DispatchingTransformer(TransformerEncoder):
     # -- routes ------------------------------------------------------------
     def _forward_hip(self, x, valid_token_mask=None):
         _, lengths = self._mask_info(valid_token_mask)
+        if self._graphable(x):
+            return self._forward_graphed(x, valid_token_mask, lengths)
         return self.forward_layers(x, valid_token_mask, lengths)
+
+    # -- graph replay (the counterpart of the reference's "reduce-overhead" routes)
+    def _graphable(self, x) -> bool:
+        return (self.use_graphs and os.environ.get("TECHJAM_AMD_GRAPHS", "1") != "0"
+                and x.is_cuda and x.ndim == 3 and x.is_contiguous() and not torch.is_grad_enabled()
+                and x.shape[0] * x.shape[1] <= GRAPH_MAX_TOKENS
+                and not torch.cuda.is_current_stream_capturing())
+
+    def _forward_graphed(self, x, mask, lengths):
+        key = graph_key(x, mask, lengths, (self.gemm_operands, torch.get_float32_matmul_precision(),
+                                           bool(torch.backends.cuda.matmul.allow_tf32)))
+        if key in self._graph_failures:
+            return self.forward_layers(x, mask, lengths)
+        signature = weights_signature(self)
+        graphed = self._graphs.get(key)
+        if graphed is None or graphed.signature != signature or not graphed.matches(x, mask, lengths):
+            self._graphs.pop(key, None)
+            if len(self._graphs) >= GRAPH_CACHE_SIZE:
+                self._graphs.pop(next(iter(self._graphs)))
+            try:
+                graphed = GraphedForward(self.forward_layers, x, mask, lengths, signature)
+            except UnsupportedCaseError:
+                raise
+            except Exception as err:  # capture refused: this signature runs eagerly from now on
+                self._graph_failures[key] = f"{type(err).__name__}: {err}"
+                return self.forward_layers(x, mask, lengths)
+            self._graphs[key] = graphed
+        return graphed(x, mask, lengths)
 
     def _forward_case_6(self, x, valid_token_mask=None):
         chunk = choose_batch_chunk_size(x, self.config.num_heads, score_copies=0, activation_copies=12)

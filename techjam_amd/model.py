@@ -49,6 +49,26 @@ def config_key(config) -> tuple:
             config.ffn_dim, config.causal, config.num_layers)
 
 
+#: Float32 GEMMs of at most this many multiply-adds run on rocBLAS: below it
+#: hipBLASLt's kernels sit at a ~19 us floor on this stack (256x256x256:
+#: 26 us, rocBLAS 8 us, and exact fp32); above ~2^30 hipBLASLt's fast mode
+#: wins (8192x512x1536: 51 us, rocBLAS 100 us).
+SMALL_GEMM_MACS = 1 << 29
+
+
+def _linear_f32(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``F.linear`` on float32, with small GEMMs routed to rocBLAS."""
+    if (x.is_cuda and x.dtype == torch.float32
+            and (x.numel() // max(1, x.shape[-1])) * weight.shape[0] * weight.shape[1] <= SMALL_GEMM_MACS):
+        prev = torch.backends.cuda.preferred_blas_library()
+        torch.backends.cuda.preferred_blas_library("cublas")  # the rocBLAS backend on ROCm
+        try:
+            return F.linear(x, weight, bias)
+        finally:
+            torch.backends.cuda.preferred_blas_library(prev)
+    return F.linear(x, weight, bias)
+
+
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor]) -> torch.Tensor:
     """``F.linear``; when float32 matmuls may use the faster hipBLASLt mode
     (``torch.get_float32_matmul_precision() != "highest"``, the reference
@@ -56,8 +76,8 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor]) 
     because the fused-bias GEMM ignores that mode on this stack (16384x1024 by
     1024x3072: 0.72 ms fused either way, 0.29 ms bias-free in the fast mode)."""
     if bias is None or x.device.type != "cuda" or torch.get_float32_matmul_precision() == "highest":
-        return F.linear(x, weight, bias)
-    y = F.linear(x, weight)
+        return _linear_f32(x, weight, bias)
+    y = _linear_f32(x, weight)
     y += bias
     return y
 
@@ -80,7 +100,7 @@ def project(x: torch.Tensor, weight: torch.Tensor, owner: nn.Module, key: str,
     float16 ``x`` runs on fp16 operands (the weight's cached fp16 copy) with
     fp32 accumulation, its result in ``out_dtype`` (default float16)."""
     if x.dtype != torch.float16:
-        return F.linear(x, weight)
+        return _linear_f32(x, weight)
     w16 = fp16_weight(owner, key, weight)
     if out_dtype in (None, torch.float16):
         return F.linear(x, w16)
@@ -196,11 +216,11 @@ class EncoderBlock(nn.Module):
 
         attn = self.attention
         ctx = attn.context(self.norm1(x), valid_token_mask, causal, valid_len)
-        y = F.linear(ctx, attn.out_proj.weight)
+        y = _linear_f32(ctx, attn.out_proj.weight)
         x = _must(bias_residual(x, y, attn.out_proj.bias, valid_len, MODE_ZERO_Y, out=y))
-        h = F.linear(self.norm2(x), self.ffn_in.weight)
+        h = _linear_f32(self.norm2(x), self.ffn_in.weight)
         _must(bias_gelu(h, self.ffn_in.bias))
-        y = F.linear(h, self.ffn_out.weight)
+        y = _linear_f32(h, self.ffn_out.weight)
         return _must(bias_residual(x, y, self.ffn_out.bias, valid_len, MODE_ZERO_OUT, out=y))
 
     def _forward_fused_norms(self, x, xn, valid_token_mask, causal, valid_len, next_norm, last,

@@ -1,0 +1,108 @@
+"""Graph replay of the dispatcher's exact-attention forward.
+
+Every replay is checked against the eager forward of the same model on the
+same inputs (bitwise: same kernels in the same order), with eager work and
+synchronisations between replays, and results of earlier calls are checked
+to survive later replays.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle.model import DenseTransformer, generate_random_case
+from oracle.model import TransformerConfig as OracleConfig
+
+pytestmark = pytest.mark.gpu
+
+C1 = OracleConfig(2, 128, 256, 4, 1024, 1, True)
+C2 = OracleConfig(8, 1024, 512, 8, 2048, 4, True)
+
+
+def _model(cfg, seed, cuda):
+    from techjam_amd.dispatcher import DispatchingTransformer
+
+    torch.manual_seed(seed)
+    base = DenseTransformer(cfg).eval()
+    cand = DispatchingTransformer(cfg).eval()
+    cand.load_state_dict(base.state_dict())
+    return cand.to(cuda)
+
+
+def _inputs(cfg, seed, cuda):
+    x, mask = generate_random_case(cfg, torch.device("cpu"), torch.float32, seed, 0.5, 1.0)
+    return x.to(cuda), mask.to(cuda)
+
+
+def _eager(model, x, mask):
+    model.use_graphs = False
+    try:
+        return model(x, mask)
+    finally:
+        model.use_graphs = True
+
+
+@pytest.mark.parametrize("cfg,operands", [(C1, "fp32"), (C2, "fp32"), (C2, "fp16")],
+                         ids=["C1", "C2", "C2-fp16-operands"])
+def test_every_replay_matches_eager(cuda, cfg, operands, monkeypatch):
+    from techjam_amd import dispatcher as D
+
+    monkeypatch.setattr(D, "GRAPH_MAX_TOKENS", 8192)   # C2 runs eagerly by default
+    model = _model(cfg, 11, cuda)
+    model.gemm_operands = operands
+    inputs = [_inputs(cfg, 1234 + i, cuda) for i in range(4)]
+    kept = []
+    with torch.inference_mode():
+        for x, mask in inputs:
+            got = model(x, mask)
+            torch.cuda.synchronize()
+            ref = _eager(model, x, mask)          # eager work between replays
+            torch.cuda.synchronize()
+            assert torch.equal(got, ref)
+            kept.append((got, ref))
+        for got, ref in kept:                      # earlier results were not overwritten
+            assert torch.equal(got, ref)
+    assert len(model._graphs) == 1 and not model._graph_failures
+
+
+def test_new_weights_are_captured_again(cuda):
+    model = _model(C1, 11, cuda)
+    x, mask = _inputs(C1, 99, cuda)
+    with torch.inference_mode():
+        first = model(x, mask)
+        other = _model(C1, 12, cuda)
+        model.load_state_dict(other.state_dict())
+        after_load = model(x, mask)
+        assert torch.equal(after_load, _eager(other, x, mask))
+        assert not torch.equal(after_load, first)
+        with torch.no_grad():
+            model.layers[0].ffn_in.weight.mul_(0.5)  # in place: same address, new version
+        after_edit = model(x, mask)
+        assert torch.equal(after_edit, _eager(model, x, mask))
+        assert not torch.equal(after_edit, after_load)
+
+
+def test_masks_and_unmasked_inputs(cuda):
+    model = _model(C1, 5, cuda)
+    x, mask = _inputs(C1, 7, cuda)
+    with torch.inference_mode():
+        for m in (mask, mask.clone().fill_(True), None):
+            assert torch.equal(model(x, m), _eager(model, x, m))
+    assert len(model._graphs) == 2  # a capture with a length vector, one without
+
+
+def test_graph_replay_is_off_for_large_inputs_and_by_environment(cuda, monkeypatch):
+    from techjam_amd import dispatcher as D
+
+    model = _model(C1, 5, cuda)
+    x, mask = _inputs(C1, 7, cuda)
+    monkeypatch.setattr(D, "GRAPH_MAX_TOKENS", 128)
+    with torch.inference_mode():
+        model(x, mask)
+    assert not model._graphs
+    monkeypatch.setattr(D, "GRAPH_MAX_TOKENS", 4096)
+    monkeypatch.setenv("TECHJAM_AMD_GRAPHS", "0")
+    with torch.inference_mode():
+        model(x, mask)
+    assert not model._graphs
