@@ -284,7 +284,8 @@ class DispatchingTransformer(TransformerEncoder):
 
     def _forward_graphed(self, x, mask, lengths):
         key = graph_key(x, mask, lengths, (self.gemm_operands, torch.get_float32_matmul_precision(),
-                                           bool(torch.backends.cuda.matmul.allow_tf32)))
+                                           bool(torch.backends.cuda.matmul.allow_tf32),
+                                           str(torch.backends.cuda.preferred_blas_library())))
         if key in self._graph_failures:
             return self.forward_layers(x, mask, lengths)
         signature = weights_signature(self)

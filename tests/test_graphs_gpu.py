@@ -92,6 +92,20 @@ def test_masks_and_unmasked_inputs(cuda):
     assert len(model._graphs) == 2  # a capture with a length vector, one without
 
 
+def test_numerics_flags_select_their_own_capture(cuda):
+    model = _model(C1, 5, cuda)
+    x, mask = _inputs(C1, 7, cuda)
+    old = torch.get_float32_matmul_precision()
+    try:
+        with torch.inference_mode():
+            for precision in ("highest", "high"):
+                torch.set_float32_matmul_precision(precision)
+                assert torch.equal(model(x, mask), _eager(model, x, mask))
+    finally:
+        torch.set_float32_matmul_precision(old)
+    assert len(model._graphs) == 2
+
+
 def test_graph_replay_is_off_for_large_inputs_and_by_environment(cuda, monkeypatch):
     from techjam_amd import dispatcher as D
 
