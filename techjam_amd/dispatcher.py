@@ -46,7 +46,7 @@ from .implementations.extreme import (
 )
 from .implementations.sdpa import PackedQKVSDPASelfAttention, StridedSDPASelfAttention
 from .infra import BENCHMARK_CONFIGS, CandidateSpec, OfficialCase, load_official_cases
-from .kernels.attention import SUPPORTED_HEAD_DIMS
+from .kernels.attention import SUPPORTED_HEAD_DIMS, kernel_head_dim
 from .graphs import GraphedForward, graph_key, weights_signature
 from .model import TransformerConfig, TransformerEncoder, config_key
 
@@ -153,9 +153,9 @@ def select_route(
     if dtype not in SUPPORTED_DTYPES:
         return RouteDecision(case_id, UNSUPPORTED_BACKEND, None, f"dtype {dtype} is not supported")
     head_dim = config.d_model // config.num_heads
-    if head_dim not in SUPPORTED_HEAD_DIMS:
+    if kernel_head_dim(head_dim) is None:
         return RouteDecision(case_id, UNSUPPORTED_BACKEND, None,
-                             f"head_dim {head_dim} is not implemented (supported: {SUPPORTED_HEAD_DIMS})")
+                             f"head_dim {head_dim} is not implemented (at most {SUPPORTED_HEAD_DIMS[-1]})")
     if case_id in EXTREME_CASES:
         if case_id == 6 and dtype != torch.float32:
             return RouteDecision(case_id, UNSUPPORTED_BACKEND, None, "case 6 is validated in float32")
@@ -425,7 +425,7 @@ CANDIDATE = CandidateSpec(
         "attention with per-head exact fallback for case 14."
     ),
     self_compiling=True,
-    unsupported_official_cases=(7, 8, 11),
+    unsupported_official_cases=(8,),
     official_case_dtypes=((6, ("float32",)), (14, ("float16", "float32"))),
     candidate_only_official_cases=(14,),
     default_input_scale_only_cases=(14,),

@@ -16,6 +16,7 @@ from dataclasses import dataclass
 from typing import Optional, Union
 
 import torch
+import torch.nn.functional as F
 
 from ..errors import UnsupportedCaseError
 from . import _lib
@@ -68,10 +69,21 @@ def _check_qkv(q, k, v):
         raise UnsupportedCaseError(f"dtype {q.dtype} is not supported (float32 or float16)")
     if k.dtype != q.dtype or v.dtype != q.dtype:
         raise ValueError("q, k, v must share a dtype")
-    if q.shape[-1] not in SUPPORTED_HEAD_DIMS:
+    if kernel_head_dim(q.shape[-1]) is None:
         raise UnsupportedCaseError(
-            f"head_dim {q.shape[-1]} is not supported (supported: {SUPPORTED_HEAD_DIMS})"
+            f"head_dim {q.shape[-1]} is not supported (at most {SUPPORTED_HEAD_DIMS[-1]}; "
+            f"{SUPPORTED_HEAD_DIMS} natively, others zero-padded)"
         )
+
+
+def kernel_head_dim(d: int) -> Optional[int]:
+    """The kernel head_dim that serves ``d``: ``d`` itself when the kernel
+    has it, else the next of ``SUPPORTED_HEAD_DIMS`` (q, k, v zero-padded to
+    it), or ``None`` beyond the largest."""
+    for p in SUPPORTED_HEAD_DIMS:
+        if 0 < d <= p:
+            return p
+    return None
 
 
 def empty_like_heads(q: torch.Tensor) -> torch.Tensor:
@@ -119,6 +131,19 @@ def scaled_dot_product_attention(
     b, h, s, d = q.shape
     if scale is None:
         scale = d ** -0.5
+    dp = kernel_head_dim(d)
+    if dp != d:
+        # Zero dims add nothing to q.k and give zero output columns: pad to the
+        # kernel's head_dim (same scale) and return the first d columns.
+        if out is not None:
+            raise ValueError(f"out= is not supported for head_dim {d} (computed padded to {dp})")
+        pad = (0, dp - d)
+        q, k, v = (F.pad(t, pad) for t in (q, k, v))
+        q_bias, v_bias = (None if t is None else F.pad(t.reshape(h, d), pad).reshape(-1)
+                          for t in (q_bias, v_bias))
+        res = scaled_dot_product_attention(q, k, v, is_causal=is_causal, scale=scale, valid_len=valid_len,
+                                           row_limit=row_limit, qk_split=qk_split, q_bias=q_bias, v_bias=v_bias)
+        return res[..., :d]
     q, k, v = _kernel_view(q), _kernel_view(k), _kernel_view(v)
     if out is None:
         out = empty_like_heads(q)

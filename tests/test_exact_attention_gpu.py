@@ -56,6 +56,23 @@ def test_matches_brute_force(cuda, s, causal, d):
     _assert_close(got, ref, max_abs=4e-3, what=f"s={s} d={d} causal={causal}")
 
 
+@pytest.mark.parametrize("d", [8, 16, 40, 100])
+@pytest.mark.parametrize("causal", [True, False])
+def test_head_dims_served_by_zero_padding(cuda, causal, d):
+    b, h, s = 2, 3, 200
+    q, k, v = (_draw((b, h, s, d), seed) for seed in (4, 5, 6))
+    ref = brute_force_attention(q, k, v, d ** -0.5, causal)
+    got = _run(q, k, v, cuda, is_causal=causal)
+    assert got.shape == (b, h, s, d)
+    _assert_close(got, ref, max_abs=4e-3, what=f"d={d} causal={causal}")
+    lens = torch.tensor([200, 77], dtype=torch.int32)
+    got = _run(q, k, v, cuda, is_causal=causal, valid_len=lens.to(cuda))
+    for i, n in enumerate(lens.tolist()):
+        ref_i = brute_force_attention(q[i:i + 1, :, :n], k[i:i + 1, :, :n], v[i:i + 1, :, :n], d ** -0.5, causal)
+        _assert_close(got[i:i + 1, :, :n], ref_i, max_abs=4e-3, what=f"d={d} sample {i}")
+        assert float(got[i, :, n:].abs().max().cpu()) == 0.0 if n < s else True
+
+
 @pytest.mark.parametrize("causal", [True, False])
 def test_right_padding_valid_lengths(cuda, causal):
     b, h, s, d = 4, 2, 200, 64
