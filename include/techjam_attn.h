@@ -73,7 +73,8 @@ const char* tj_error_string(int code);
  * input type. Heads with qk_split[b*H + h] != 0 form QK^T from a two-term
  * fp16 expansion of q and k (three MFMAs), which keeps fp32-level score
  * accuracy for wide score ranges (sigma of the scaled scores >~ 2).
- * head_dim D must be 32, 64 or 128.
+ * head_dim D must be 32, 64, 128 or 256 (256: one workgroup per CU; no
+ * qk_split, which returns TJ_ERR_UNSUPPORTED).
  *
  * dtype: TJ_F32 or TJ_F16 (q, k, v and o share it).
  * valid_len: device int32[B] or NULL. row_limit, qk_split: device

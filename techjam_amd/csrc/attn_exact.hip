@@ -422,7 +422,7 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
 }
 
 template <typename T, int HD, int QB, bool SPLIT_OK>
-__global__ __launch_bounds__(NT, 2) void attn_fwd_kernel(AttnArgs a) {
+__global__ __launch_bounds__(NT, (HD > 128 ? 1 : 2)) void attn_fwd_kernel(AttnArgs a) {
   __shared__ Smem<HD, SPLIT_OK> sm;
 
   // XCD-aware tile order: ids x, x+8, x+16, ... run on XCD x.
@@ -493,7 +493,7 @@ int launch_qb(AttnArgs a, hipStream_t stream) {
   const int64_t per_xcd = (bhn + kNumXcd - 1) / kNumXcd;
   const int64_t grid = a.balanced ? bhn * a.n_mtiles : kNumXcd * (per_xcd + a.group - 1) * a.n_mtiles;
   if (grid * NT >= (int64_t(1) << 32)) return TJ_ERR_SHAPE;
-  if constexpr (QB == 1) {
+  if constexpr (QB == 1 && HD <= 128) {
     if (a.qk_split != nullptr) {
       hipLaunchKernelGGL((attn_fwd_kernel<T, HD, QB, true>), dim3(uint32_t(grid)), dim3(NT), 0, stream, a);
       return tjh::launch_status();
@@ -523,6 +523,7 @@ int dispatch_hd(const AttnArgs& a, int64_t D, hipStream_t stream) {
     case 32: return launch<T, 32>(a, stream);
     case 64: return launch<T, 64>(a, stream);
     case 128: return launch<T, 128>(a, stream);
+    case 256: return a.qk_split != nullptr ? TJ_ERR_UNSUPPORTED : launch<T, 256>(a, stream);
     default: return TJ_ERR_UNSUPPORTED;
   }
 }
@@ -542,7 +543,7 @@ int attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype, in
   // Tile indices fit 31 bits; the launch also checks that its grid fits the
   // 32-bit dispatch size.
   if (B * H * ((S + 127) / 128) >= (int64_t(1) << 31) || S >= (int64_t(1) << 30)) return TJ_ERR_SHAPE;
-  if (D != 32 && D != 64 && D != 128) return TJ_ERR_UNSUPPORTED;
+  if (D != 32 && D != 64 && D != 128 && D != 256) return TJ_ERR_UNSUPPORTED;
   if (B == 0 || S == 0) return TJ_OK;
   if (!q || !k || !v || !o) return TJ_ERR_SHAPE;
   if (!tjh::view_ok(q, q_strides, dtype) || !tjh::view_ok(k, k_strides, dtype) ||

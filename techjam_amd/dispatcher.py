@@ -9,7 +9,7 @@ Keeps the public interface of the reference's ``src/dispatcher.py:39-818`` --
 
 * every attention call runs the gfx950 HIP kernels through the C ABI; there is
   no ``torch.compile`` route and no dense fallback. Requests the kernels do not
-  implement (CPU tensors, other GPUs, head sizes outside {32, 64, 128},
+  implement (CPU tensors, other GPUs, head sizes above 256,
   bfloat16, non-prefix masks) raise ``UnsupportedCaseError`` before any
   allocation, and a failing kernel call is recorded in ``compile_failures``
   and re-raised;
@@ -425,7 +425,7 @@ CANDIDATE = CandidateSpec(
         "attention with per-head exact fallback for case 14."
     ),
     self_compiling=True,
-    unsupported_official_cases=(8,),
+    unsupported_official_cases=(),
     official_case_dtypes=((6, ("float32",)), (14, ("float16", "float32"))),
     candidate_only_official_cases=(14,),
     default_input_scale_only_cases=(14,),

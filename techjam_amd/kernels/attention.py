@@ -21,7 +21,7 @@ import torch.nn.functional as F
 from ..errors import UnsupportedCaseError
 from . import _lib
 
-SUPPORTED_HEAD_DIMS = (32, 64, 128)
+SUPPORTED_HEAD_DIMS = (32, 64, 128, 256)
 
 _DTYPES = {torch.float32: _lib.TJ_F32, torch.float16: _lib.TJ_F16}
 

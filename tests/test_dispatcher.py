@@ -58,10 +58,10 @@ def test_refuses_what_the_kernels_do_not_implement():
         (official(1), dict(GPU, device_type="cpu")),
         (official(1), dict(GPU, device_arch="gfx942")),
         (official(1), dict(GPU)),          # bfloat16 below
-        (official(8), dict(GPU)),          # head_dim 256
         (official(6), dict(GPU)),          # case 6 in float16
+        (TransformerConfig(2, 64, 1024, 2, 64, 1, True), dict(GPU)),   # head_dim 512
     ]
-    dtypes = [torch.float32, torch.float32, torch.bfloat16, torch.float32, torch.float16]
+    dtypes = [torch.float32, torch.float32, torch.bfloat16, torch.float16, torch.float32]
     for (cfg, contract), dt in zip(cases, dtypes):
         assert D.select_route(cfg, dtype=dt, **contract).backend == D.UNSUPPORTED_BACKEND
 
@@ -69,11 +69,11 @@ def test_refuses_what_the_kernels_do_not_implement():
 def test_small_head_dims_take_the_exact_route_padded():
     from techjam_amd.kernels.attention import kernel_head_dim
 
-    for case_id in (7, 11):                # head_dim 8
+    for case_id in (7, 8, 11):             # head_dim 8, 256, 8
         r = D.select_route(official(case_id), dtype=torch.float32, **GPU)
         assert r.backend == D.HIP_EXACT_BACKEND
-    assert [kernel_head_dim(d) for d in (1, 8, 32, 33, 64, 65, 100, 128, 129, 256)] == \
-        [32, 32, 32, 64, 64, 128, 128, 128, None, None]
+    assert [kernel_head_dim(d) for d in (1, 8, 32, 33, 64, 65, 100, 128, 129, 256, 257)] == \
+        [32, 32, 32, 64, 64, 128, 128, 128, 256, 256, None]
 
 
 def test_generic_shapes_take_the_exact_route():
@@ -303,13 +303,15 @@ def test_candidate_loads_and_validates():
 
 
 def test_candidate_refuses_before_allocation():
-    from techjam_amd.infra import validate_candidate_execution
+    from techjam_amd.infra import CandidateSpec, validate_candidate_execution
 
     spec = D.CANDIDATE
     with pytest.raises(ValueError, match="compiles itself"):
         validate_candidate_execution(spec, 1, compile_user=True)
+    refusing = CandidateSpec("r", D.DispatchingTransformer, "o", "d", self_compiling=True,
+                             unsupported_official_cases=(8,))
     with pytest.raises(ValueError, match="does not support"):
-        validate_candidate_execution(spec, 8, compile_user=False, device_type="cuda")
+        validate_candidate_execution(refusing, 8, compile_user=False, device_type="cuda")
     with pytest.raises(ValueError, match="only with"):
         validate_candidate_execution(spec, 6, compile_user=False, dtype_name="float16", device_type="cuda")
     with pytest.raises(ValueError, match="dense baseline"):
@@ -317,7 +319,8 @@ def test_candidate_refuses_before_allocation():
     with pytest.raises(ValueError, match="GPU"):
         validate_candidate_execution(spec, 1, compile_user=False, dtype_name="float32", device_type="cpu")
     validate_candidate_execution(spec, 1, compile_user=False, dtype_name="float32", device_type="cuda")
-    validate_candidate_execution(spec, 7, compile_user=False, dtype_name="float32", device_type="cuda")
+    for case_id in (7, 8, 11):
+        validate_candidate_execution(spec, case_id, compile_user=False, dtype_name="float32", device_type="cuda")
 
 
 def test_candidate_spec_validation_rules():

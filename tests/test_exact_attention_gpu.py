@@ -45,7 +45,7 @@ def _run(q, k, v, dev, **kw):
     return out
 
 
-@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("d", [32, 64, 128, 256])
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("s", [1, 7, 64, 100, 129, 300])
 def test_matches_brute_force(cuda, s, causal, d):
@@ -56,7 +56,7 @@ def test_matches_brute_force(cuda, s, causal, d):
     _assert_close(got, ref, max_abs=4e-3, what=f"s={s} d={d} causal={causal}")
 
 
-@pytest.mark.parametrize("d", [8, 16, 40, 100])
+@pytest.mark.parametrize("d", [8, 16, 40, 100, 160])
 @pytest.mark.parametrize("causal", [True, False])
 def test_head_dims_served_by_zero_padding(cuda, causal, d):
     b, h, s = 2, 3, 200

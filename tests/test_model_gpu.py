@@ -89,7 +89,7 @@ def test_config_2_packed_qkv_four_layers(cuda):
     _check(cfg, (1234, 1235), 0.5, cuda)
 
 
-@pytest.mark.parametrize("case_id", [1, 7, 9, 10, 11, 12, 13])
+@pytest.mark.parametrize("case_id", [1, 7, 8, 9, 10, 11, 12, 13])
 def test_official_cases_with_supported_head_dims(cuda, case_id):
     from techjam_amd.infra import load_official_cases
 
