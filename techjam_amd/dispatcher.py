@@ -278,7 +278,8 @@ class DispatchingTransformer(TransformerEncoder):
     # -- graph replay (the counterpart of the reference's "reduce-overhead" routes)
     def _graphable(self, x) -> bool:
         return (self.use_graphs and os.environ.get("TECHJAM_AMD_GRAPHS", "1") != "0"
-                and x.is_cuda and x.ndim == 3 and x.is_contiguous() and not torch.is_grad_enabled()
+                and x.is_cuda and x.device.index == torch.cuda.current_device()
+                and x.ndim == 3 and x.is_contiguous() and not torch.is_grad_enabled()
                 and x.shape[0] * x.shape[1] <= GRAPH_MAX_TOKENS
                 and not torch.cuda.is_current_stream_capturing())
 
