@@ -89,13 +89,15 @@ def test_config_2_packed_qkv_four_layers(cuda):
     _check(cfg, (1234, 1235), 0.5, cuda)
 
 
-@pytest.mark.parametrize("case_id", [1, 7, 8, 9, 10, 11, 12, 13])
-def test_official_cases_with_supported_head_dims(cuda, case_id):
+@pytest.mark.parametrize("case_id", list(range(1, 14)))
+def test_official_cases(cuda, case_id):
+    """Official cases 1-13 at their own sizes (case 6: 10000 samples through
+    the batch-streamed route, oracle on the GPU)."""
     from techjam_amd.infra import load_official_cases
 
     c = load_official_cases()[case_id]
     cfg = OracleConfig(c.batch_size, c.seq_len, c.qkv_dim, c.heads, c.ffn_dim, c.layers, c.causal)
-    _check(cfg, (1234,), 0.3, cuda)
+    _check(cfg, (1234,), 0.3, cuda, oracle_on_gpu=case_id == 6)
 
 
 def test_config_2_under_the_reference_harness_matmul_flags(cuda):
