@@ -31,6 +31,8 @@
 //     (at most two such groups) is interleaved group by group throughout.
 //     Launches with row limits, whose work sits on a few (b, h), and launches
 //     with fewer than eight (b, h) spread every (b, h) over all XCDs.
+//     The (b, h) ranges are taken in sample-fastest order, so each XCD holds
+//     an even mix of the samples' valid lengths.
 //   * Heads flagged in qk_split compute QK^T from a two-term fp16 expansion of
 //     q and k (x = hi + lo, both fp16) with three MFMAs -- hi.hi + hi.lo +
 //     lo.hi -- which restores fp32-level score accuracy where the score range
@@ -464,6 +466,9 @@ __global__ __launch_bounds__(NT, (HD > 128 ? 1 : 2)) void attn_fwd_kernel(AttnAr
       bh = bh0 + g0 + rr % gs;
     }
     mt = a.n_mtiles - 1 - mrev;
+    // Logical (b, h) order runs over samples first, so every XCD's range
+    // mixes the samples' valid lengths evenly.
+    bh = (bh % a.B) * a.H + bh / a.B;
   }
   const int b = bh / a.H;
   const int h = bh % a.H;
