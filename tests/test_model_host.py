@@ -37,3 +37,34 @@ def test_project_rounds_operands_for_fp16_inputs():
     assert y.dtype == torch.float16 and y.shape == (2, 3, 4)
     ref = x.half().double() @ lin.weight.detach().half().double().t()
     assert torch.allclose(y.double(), ref, atol=2e-3, rtol=2e-3)
+
+
+def test_weights_signature_tracks_in_place_edits_and_replacement():
+    from techjam_amd.graphs import weights_signature
+
+    net = torch.nn.Sequential(torch.nn.Linear(4, 4), torch.nn.LayerNorm(4))
+    net.register_buffer("cache", torch.zeros(3))
+    sig = weights_signature(net)
+    assert weights_signature(net) == sig
+    with torch.no_grad():
+        net[0].weight.add_(1.0)
+    edited = weights_signature(net)
+    assert edited != sig
+    net[1].bias = torch.nn.Parameter(torch.ones(4))
+    assert weights_signature(net) != edited
+    net.cache = torch.ones(3)                       # a replaced buffer counts too
+    assert len(weights_signature(net)) == len(sig)
+
+
+def test_graph_key_separates_shapes_dtypes_and_flags():
+    from techjam_amd.graphs import graph_key
+
+    x = torch.zeros(2, 8, 4)
+    m = torch.ones(2, 8, dtype=torch.bool)
+    lens = torch.full((2,), 8, dtype=torch.int32)
+    base = graph_key(x, m, lens, ("fp32",))
+    assert base == graph_key(x.clone(), m.clone(), lens.clone(), ("fp32",))
+    assert base != graph_key(x, None, None, ("fp32",))
+    assert base != graph_key(x.half(), m, lens, ("fp32",))
+    assert base != graph_key(torch.zeros(2, 9, 4), m, lens, ("fp32",))
+    assert base != graph_key(x, m, lens, ("fp16",))
