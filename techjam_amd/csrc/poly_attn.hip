@@ -11,9 +11,9 @@
 //   S_quad[(i,j), v] += sum_t b_ti b_tj v_tv,  S_lin[j, v] += sum_t b_tj v_tv,
 //   G[i, j] += sum_t b_ti b_tj,  z[j] += sum_t b_tj,  S_const[v] += sum_t v_tv.
 //
-// Launches advance four chunks at a time; in launch L every head owns 27
+// Launches advance KG = 8 chunks at a time; in launch L every head owns 47
 // workgroups with four roles:
-//   * apply (4 per chunk, 128 rows each, for the four chunks whose start
+//   * apply (4 per chunk, 128 rows each, for the eight chunks whose start
 //     states the previous launch produced): quadratic term as
 //       y^T = sum_i S_i^T (a_i * a^T)  (S_i = rows (i, .) of S_quad),
 //     i.e. 64 MFMA GEMMs whose B operand is the fp16 product a_i*a_j built in
@@ -21,19 +21,22 @@
 //     as three more small GEMMs; the exact diagonal block like the exact
 //     kernel (S^T = b a^T in registers, no max subtraction).
 //   * quad update (6 per head): S_i += (b_i * b)^T v over the tokens of
-//     chunks [4L, 4L + 4), accumulated straight into MFMA accumulators that
+//     chunks [8L, 8L + 8), accumulated straight into MFMA accumulators that
 //     hold the fp32 master in its register image (the master's memory layout
 //     IS the accumulator layout, so loading and storing it is straight 16-byte
 //     copies, once per launch). After each chunk it writes the fp16 shadow of
 //     the state the apply of the next chunk reads.
 //   * small-state update (1 per head): S_lin, G, z, S_const, likewise.
-//   * token images (4 per head): b = k*sqrt(scale) and v of the chunks the
+//   * token images (8 per head): b = k*sqrt(scale) and v of the chunks the
 //     next launch folds in, converted once to fp16 tiles laid out as the
 //     update roles' LDS image, which those roles then stream with direct
 //     global->LDS copies.
-// State c (before chunk c) lives in shadow slot c % 8: a launch reads the
-// slots of states 4L-3 .. 4L and writes those of 4L+1 .. 4L+4, so applies and
-// updates of one launch never touch the same slot.
+// State c (before chunk c) lives in shadow slot c % 16: a launch reads the
+// slots of states 8L-7 .. 8L and writes those of 8L+1 .. 8L+8, so applies and
+// updates of one launch never touch the same slot. Eight chunks per launch
+// load and store each master half as often as four (the polynomial call on
+// 64 heads of 65536 tokens: 5.8-6.1 -> 5.4-5.5 ms, bitwise the same); twelve
+// or sixteen gain another ~1 % for 0.25-0.5 GiB more shadow slots.
 // Heads whose guard flag is 0 exit at once (the exact kernel covers them).
 #include <type_traits>
 
@@ -47,7 +50,7 @@ constexpr int PC = 512;        // chunk length
 constexpr int PT = 256;        // threads per workgroup
 constexpr int NAPPLY = 4;      // apply workgroups per head and chunk (128 rows each)
 constexpr int NUPD = 6;        // quad-update workgroups per head (4 for i < 32, 2 for i >= 32)
-constexpr int KG = 4;          // chunks per launch (update sub-chunks, apply groups)
+constexpr int KG = 8;          // chunks per launch (update sub-chunks, apply groups)
 constexpr int NSLOT = 2 * KG;  // shadow slots: state_c lives in slot c % NSLOT
 constexpr int NCONV = KG;      // token-image workgroups per head (one chunk each)
 constexpr int NROLE = KG * NAPPLY + NUPD + 1 + NCONV;
@@ -68,7 +71,7 @@ constexpr size_t kZsShadow = kGramShadow + NSLOT * PD * PD * 2;   // fp32 [NSLOT
 // Token images: the k (scaled) and v tiles the update roles of a launch fold
 // in, written once by the previous launch as fp16 LDS images (see TokTile).
 constexpr int kTileImg = 2 * PD * 64 * 2;                          // [b^T | v^T] of 64 tokens
-constexpr size_t kTokImgBytes = size_t(KG) * (PC / 64) * kTileImg;  // one launch: 512 KiB
+constexpr size_t kTokImgBytes = size_t(KG) * (PC / 64) * kTileImg;  // one launch: 1 MiB
 constexpr size_t kTokImg = (kZsShadow + NSLOT * 128 * 4 + 255) & ~size_t(255);  // [2][kTokImgBytes]
 constexpr size_t kPerHead = kTokImg + 2 * kTokImgBytes;
 
@@ -823,15 +826,38 @@ __global__ __launch_bounds__(PT, 2) void poly_chunk_kernel(PolyArgs a) {
   }
 }
 
-__global__ void zero_kernel(float4_t* p, size_t n) {
-  for (size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x)
-    p[i] = float4_t{0.f, 0.f, 0.f, 0.f};
+// Clears what must start at zero in every head's workspace: the fp32 masters
+// and shadow slot 0 (state 0, read by launch 0's apply of chunk 0). Every
+// other slot and the token images are written before they are read. The
+// masters and quad slot 0 are one contiguous range, split over kZeroParts
+// workgroups per head; part 0 also clears the small shadows' slot 0.
+constexpr int kZeroParts = 8;
+constexpr size_t kZeroMain = kQuadShadow + size_t(PD) * PD * PD * 2;  // masters + quad slot 0
+
+__device__ __forceinline__ void zero_range(uint8_t* p, size_t bytes, size_t lane, size_t lanes) {
+  float4_t* q = reinterpret_cast<float4_t*>(p);
+  for (size_t i = lane; i < bytes / 16; i += lanes) q[i] = float4_t{0.f, 0.f, 0.f, 0.f};
+}
+
+__global__ void zero_state_kernel(uint8_t* ws, int M) {
+  const int m = blockIdx.x / kZeroParts, part = blockIdx.x % kZeroParts;
+  if (m >= M) return;
+  uint8_t* h = ws + size_t(m) * kPerHead;
+  constexpr size_t kSlice = kZeroMain / kZeroParts;
+  static_assert(kZeroMain % (16 * kZeroParts) == 0, "slices of whole float4s");
+  zero_range(h + part * kSlice, kSlice, threadIdx.x, blockDim.x);
+  if (part == 0) {
+    zero_range(h + kLinShadow, size_t(PD) * PD * 2, threadIdx.x, blockDim.x);
+    zero_range(h + kGramShadow, size_t(PD) * PD * 2, threadIdx.x, blockDim.x);
+    zero_range(h + kZsShadow, 128 * 4, threadIdx.x, blockDim.x);
+  }
 }
 
 template <typename T>
 int run(PolyArgs a, size_t ws_bytes, hipStream_t stream) {
-  hipLaunchKernelGGL(zero_kernel, dim3(1024), dim3(256), 0, stream, reinterpret_cast<float4_t*>(a.ws),
-                     ws_bytes / 16);
+  (void)ws_bytes;
+  hipLaunchKernelGGL(zero_state_kernel, dim3(unsigned(a.M * kZeroParts)), dim3(256), 0, stream,
+                     reinterpret_cast<uint8_t*>(a.ws), a.M);
   if (hipGetLastError() != hipSuccess) return TJ_ERR_LAUNCH;
   const dim3 grid(unsigned(kNumXcd * ((a.M + kNumXcd - 1) / kNumXcd) * NROLE));
   if (a.n_chunks > 1) {  // token images of the chunks launch 0 folds in

@@ -114,6 +114,31 @@ def test_deterministic(cuda):
     assert torch.equal(a1[:, :, 512:], a2[:, :, 512:])
 
 
+@pytest.mark.parametrize("n,prefix", [(2048, 512), (1536, 0), (300, 0), (9000, 4096)])
+def test_result_does_not_depend_on_workspace_contents(cuda, n, prefix):
+    """The call clears only what must start at zero (masters, shadow slot 0);
+    a workspace full of 0xFF bytes (NaN in every float) must give the same
+    bits as a fresh one."""
+    from techjam_amd.kernels import _lib
+    from techjam_amd.kernels.attention import _DTYPES, _stream_ptr, empty_like_heads
+    from techjam_amd.kernels.poly import poly_rows, workspace_bytes
+
+    q, k, v = (t.to(cuda).contiguous() for t in _draw(1, 2, n, seed=11))
+    c = torch.tensor(hermite_coefficients(0.334), dtype=torch.float32, device=cuda).repeat(2, 1)
+    ref = poly_rows(q, k, v, 0.125, c, exact_prefix=prefix)
+    nbytes = workspace_bytes(1, 2, n, 64, 512)
+    ws = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device=cuda)
+    for _ in range(2):  # the second call sees the first call's leftovers
+        out = empty_like_heads(q)
+        code = _lib.lib().tj_poly_attn_fwd(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), _DTYPES[q.dtype], 1, 2, n, 64,
+            _lib.strides4(q), _lib.strides4(k), _lib.strides4(v), _lib.strides4(out),
+            0.125, 512, prefix, c.data_ptr(), None, ws.data_ptr(), nbytes, _stream_ptr(cuda))
+        _lib.check(code, "tj_poly_attn_fwd")
+        torch.cuda.synchronize()
+        assert torch.equal(out[:, :, prefix:], ref[:, :, prefix:])
+
+
 def test_poly_attention_forward_matches_oracle_including_prefix(cuda):
     from techjam_amd.implementations.poly_attention import poly_attention_forward
 
