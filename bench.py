@@ -12,7 +12,18 @@ Prints ONE JSON line with the driver's fields plus
                  dense fp16 MFMA peak; `traffic` is the HBM bytes per launch
                  from rocprofv3 FETCH_SIZE/WRITE_SIZE (profiles/), or null;
   cpu_baseline : the dense FP32 oracle on this host's cores over a bounded
-                 sample of the same workload (one batch element).
+                 sample of the same workload (one batch element);
+  samples_ms   : median / p90 / min / mean of the per-step HIP-event times
+                 inside the timed region;
+  memory       : peak HBM allocated during one step (inputs included);
+  accuracy     : the timed output checked on sampled heads against exact
+                 softmax attention evaluated in fp32 by torch on the GPU,
+                 with the benchmark's rule (|d| <= 2e-3 or <= 2% of |ref|);
+  extreme      : the same measurements for the extreme-length workload
+                 (guarded polynomial attention, B=4 S=65536 H=16 D=64 with
+                 one exact-fallback head per sample), timed in the same run
+                 (``--no-extreme`` skips it);
+  git, source_digest, seeds : what was measured.
 
 Also in the line: ``environment`` (host, software, device), ``gpu_state``
 (rocm-smi clocks/power/temperature sampled after the timed region) and, with
@@ -26,26 +37,32 @@ runs the default.
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import re
 import statistics
 import sys
 import time
+from dataclasses import dataclass, field
 from pathlib import Path
+from typing import Callable, List, Optional
 
 import torch
 
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
-from techjam_amd.infra.environment import collect_environment, collect_gpu_state  # noqa: E402
+from techjam_amd.infra.environment import collect_environment, collect_git, collect_gpu_state  # noqa: E402
 from techjam_amd.infra.timing import summarise_timings, time_interleaved  # noqa: E402
+from techjam_amd.infra.workload import attention_bytes, exact_attention_flops, poly_flops, random_case  # noqa: E402
 
 PEAK_MFMA_F16_TFLOPS = 2500.0   # MI355X dense fp16/bf16
 PEAK_HBM_GBS = 8000.0           # MI355X HBM3E
 
 METRIC = "attention-layer forward latency (ms) and tokens/s; % MFMA peak / % HBM BW"
+TIMING_SEED = 1234 + 100000      # the reference harness's timing-input seed (src/benchmark.py:379)
+ATOL, RTOL = 2e-3, 0.02          # torch_transformer_benchmark.py:309-319
 
 
 def parse_args():
@@ -56,6 +73,9 @@ def parse_args():
     p.add_argument("--workload", default="attn-core",
                    choices=["attn-core", "extreme", "model-c1", "model-c2", "model-c4", "copy-1gib",
                             "quad-apply", "quad-update", "causal-diag"])
+    p.add_argument("--no-extreme", action="store_true",
+                   help="with the default workload, skip the extreme-length measurement")
+    p.add_argument("--no-accuracy", action="store_true", help="skip the sampled-heads accuracy check")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-repeats", type=int, default=3)
     p.add_argument("--aa-reps", type=int, default=0,
@@ -68,6 +88,20 @@ def parse_args():
     # Opt-in: encoder GEMM operands rounded to fp16 (TF32's mantissa), fp32 accumulation.
     p.add_argument("--gemm-operands", choices=("fp32", "fp16"), default="fp32")
     return p.parse_args()
+
+
+@dataclass
+class Workload:
+    step: Callable[[], object]
+    tokens: int
+    flops: float
+    bytes_alg: float
+    config: dict
+    profile: str
+    data: str = "synthetic: q, k, v ~ N(0, 1) generated on the GPU (seed 101234)"
+    bound: Optional[str] = None
+    accuracy: Optional[Callable[[], dict]] = None
+    seeds: dict = field(default_factory=lambda: {"timing_input": TIMING_SEED})
 
 
 def traffic_from_profiles(name: str):
@@ -85,11 +119,56 @@ def traffic_from_profiles(name: str):
     return float(m.group(1)) if m else None
 
 
-def attn_core(args, dev):
+# -- accuracy: exact softmax attention in fp32 on the GPU ----------------------------
+
+def exact_rows(q, k, v, b: int, h: int, rows: torch.Tensor, scale: float) -> torch.Tensor:
+    """Causal softmax attention of query ``rows`` of head (b, h), fp32 on the device.
+
+    Plain tensor ops under matmul precision "highest": scores of the rows
+    against every key up to the last row, ``-inf`` above the diagonal, fp32
+    softmax, product with v.
+    """
+    kmax = int(rows.max()) + 1
+    qr = q[b, h].index_select(0, rows).float()
+    kk = k[b, h, :kmax].float().contiguous()
+    scores = (qr @ kk.t()) * scale
+    cols = torch.arange(kmax, device=q.device)
+    scores.masked_fill_(cols[None, :] > rows[:, None], float("-inf"))
+    return torch.softmax(scores, dim=-1) @ v[b, h, :kmax].float().contiguous()
+
+
+def check_heads(out, q, k, v, scale: float, heads, rows: torch.Tensor, what: str) -> dict:
+    """The benchmark's per-element rule on ``rows`` of each (b, h) in ``heads``."""
+    prev = torch.get_float32_matmul_precision()
+    torch.set_float32_matmul_precision("highest")
+    failed, total, max_abs = 0, 0, 0.0
+    try:
+        for b, h in heads:
+            for r0 in range(0, rows.numel(), 1024):
+                rr = rows[r0:r0 + 1024]
+                ref = exact_rows(q, k, v, b, h, rr, scale)
+                got = out[b, h].index_select(0, rr).float()
+                err = (got - ref).abs()
+                ok = torch.isfinite(got) & ((err <= ATOL) | (err <= RTOL * ref.abs()))
+                failed += int((~ok).sum())
+                total += ok.numel()
+                max_abs = max(max_abs, float(torch.nan_to_num(err, nan=float("inf")).max()))
+    finally:
+        torch.set_float32_matmul_precision(prev)
+    return {"passed": failed == 0, "failed_elements": failed, "total_elements": total, "max_abs_error": max_abs,
+            "heads_checked": [list(x) for x in heads], "rows_per_head": int(rows.numel()),
+            "tolerance": f"|d| <= {ATOL} or |d| <= {RTOL} * |ref|, finite",
+            "reference": f"exact causal softmax attention in fp32 (torch on the GPU, matmul precision "
+                         f"'highest') of the timed inputs; {what}"}
+
+
+# -- workloads -------------------------------------------------------------------------
+
+def attn_core(args, dev) -> Workload:
     from techjam_amd.kernels import scaled_dot_product_attention
 
     b, s, h, d = 64, 4096, 16, 64
-    g = torch.Generator(device=dev).manual_seed(1234 + 100000)
+    g = torch.Generator(device=dev).manual_seed(TIMING_SEED)
     q, k, v = (torch.randn(b, s, h, d, generator=g, device=dev).transpose(1, 2) for _ in range(3))
     out = torch.empty(b, s, h, d, device=dev).transpose(1, 2)
     scale = d ** -0.5
@@ -97,18 +176,64 @@ def attn_core(args, dev):
     def step():
         scaled_dot_product_attention(q, k, v, is_causal=True, scale=scale, out=out)
 
-    flops = 2.0 * d * h * b * s * (s + 1)        # QK^T + PV, lower triangle incl. diagonal
-    bytes_alg = 16.0 * b * s * h * d             # fp32 q, k, v read once, o written once
+    def accuracy():
+        heads = [(0, 0), (63, 15), (17, 9)] + [((37 * i) % b, (5 * i + 3) % h) for i in range(13)]
+        return check_heads(out, q, k, v, scale, heads, torch.arange(s, device=dev),
+                           "16 of the 1024 (b, h) heads, every row")
+
     config = {
         "workload": "attention core: exact causal SDPA, B=64 S=4096 H=16 D=64, fp32 io",
         "batch": b, "seq_len": s, "heads": h, "head_dim": d, "causal": True,
         "layout": "[B,S,H,D] storage viewed as [B,H,S,D]",
         "mfma": "fp16 operands, fp32 accumulation",
     }
-    return step, b * s, flops, bytes_alg, config, "attn_fwd_b64_s4096_h16_d64_causal.md"
+    return Workload(step, b * s, exact_attention_flops([s] * b, h, d), attention_bytes(b, s, h, d), config,
+                    "attn_fwd_b64_s4096_h16_d64_causal.md", accuracy=accuracy)
 
 
-def copy_1gib(args, dev):
+def extreme(args, dev) -> Workload:
+    """Guarded polynomial attention, B=4 S=65536 H=16 D=64; head 0 of each sample at sigma 4."""
+    from techjam_amd.implementations.poly_attention import guarded_attention
+
+    b, s, h, d = 4, 65536, 16, 64
+    g = torch.Generator(device=dev).manual_seed(TIMING_SEED)
+    q = torch.randn(b, s, h, d, generator=g, device=dev) * 0.5
+    k = torch.randn(b, s, h, d, generator=g, device=dev) * 0.5
+    v = torch.randn(b, s, h, d, generator=g, device=dev)
+    q[:, :, 0] = torch.randn(b, s, d, generator=g, device=dev) * 2.0
+    k[:, :, 0] = torch.randn(b, s, d, generator=g, device=dev) * 2.0
+    qh, kh, vh = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+    out = torch.empty(b, s, h, d, device=dev).transpose(1, 2)
+    scale = d ** -0.5
+    guards = []
+
+    def step():
+        guards[:] = [guarded_attention(qh, kh, vh, scale, out=out)[1]]
+
+    def accuracy():
+        flags = guards[0].flags.view(b, h).cpu()
+        routes = {"polynomial_heads": int(flags.sum()), "exact_fallback_heads": int((flags == 0).sum())}
+        # rows at the start, across the end of the exact prefix, and at the end
+        rows = torch.cat([torch.arange(0, 512), torch.arange(3584, 4608), torch.arange(s - 512, s)]).to(dev)
+        res = check_heads(out, qh, kh, vh, scale, [(0, 0), (3, 0), (0, 5), (1, 11), (2, 1), (3, 15)], rows,
+                          "heads (b, 0) take the exact fallback, the others the polynomial route")
+        res.update(routes)
+        res["passed"] = res["passed"] and routes == {"polynomial_heads": 60, "exact_fallback_heads": 4}
+        return res
+
+    n_poly, n_exact = b * (h - 1), b
+    flops = n_poly * poly_flops(s, d, d, 512, 4096) + exact_attention_flops([s] * n_exact, 1, d)
+    config = {
+        "workload": "extreme-length attention core: guarded degree-2 polynomial attention, "
+                    "B=4 S=65536 H=16 D=64, fp32 io, 60 polynomial heads + 4 exact fallback heads",
+        "batch": b, "seq_len": s, "heads": h, "head_dim": d, "chunk": 512, "exact_prefix": 4096,
+    }
+    return Workload(step, b * s, flops, attention_bytes(b, s, h, d), config, "poly_extreme_b4_s65536_h16_d64.md",
+                    data="synthetic: q, k ~ N(0, 0.5^2), v ~ N(0, 1), head 0 of each sample q, k ~ N(0, 2^2), "
+                         "generated on the GPU (seed 101234)", accuracy=accuracy)
+
+
+def copy_1gib(args, dev) -> Workload:
     """Plain device copy of 1 GiB: calibrates the FETCH_SIZE / WRITE_SIZE counters."""
     n = 1 << 28
     src = torch.ones(n, device=dev)
@@ -118,19 +243,19 @@ def copy_1gib(args, dev):
         dst.copy_(src)
 
     config = {"workload": "calibration: torch device copy of 2^28 fp32 (1 GiB read + 1 GiB write)"}
-    return step, n, 0.0, 2.0 * 4 * n, config, "copy_1gib_calibration.md"
+    return Workload(step, n, 0.0, 2.0 * 4 * n, config, "copy_1gib_calibration.md", bound="hbm")
 
 
 def poly_part(name):
     """One stand-alone polynomial kernel at the reference's quoted shape
     (M=32 (b, h) pairs, C=512 tokens, D=V=64, the shape its timings for
     src/kernels/poly_attention_triton.py are quoted at)."""
-    def build(args, dev):
+    def build(args, dev) -> Workload:
         from techjam_amd.kernels.poly_parts import causal_diag, quad_apply, quad_update
 
         m, c, d = 32, 512, 64
         kernel = name.replace("-", "_")
-        g = torch.Generator(device=dev).manual_seed(1234 + 100000)
+        g = torch.Generator(device=dev).manual_seed(TIMING_SEED)
         a, b, v = (torch.randn(m, c, d, generator=g, device=dev, dtype=torch.float16) * 0.2 for _ in range(3))
         state = torch.randn(m, d * d, d, generator=g, device=dev)
         shadow = torch.zeros(m, d * d, d, device=dev, dtype=torch.float16)
@@ -147,64 +272,26 @@ def poly_part(name):
                 causal_diag(a, b, v)
             flops, nbytes = 2.0 * m * d * c * (c + 1), 3 * m * c * d * 2 + m * c * (d + 1) * 4
         config = {"workload": f"stand-alone {kernel}: M={m} (b, h) pairs, C={c} tokens, D=V={d}, "
-                              "fp16 operands, fp32 state", "m": m, "chunk": c, "head_dim": d,
-                  # the update reads and writes the fp32 state once per call: HBM sets its floor
-                  "bound": "hbm" if name == "quad-update" else "mfma",
-                  "data": "synthetic: a, b, v ~ N(0, 0.2^2) fp16, state ~ N(0, 1) fp32, generated on the GPU "
-                          "(seed 101234)"}
-        return step, m * c, flops, float(nbytes), config, "poly_parts_m32_c512_d64.md#" + kernel
+                              "fp16 operands, fp32 state", "m": m, "chunk": c, "head_dim": d}
+        # the update reads and writes the fp32 state once per call: HBM sets its floor
+        return Workload(step, m * c, flops, float(nbytes), config, "poly_parts_m32_c512_d64.md#" + kernel,
+                        data="synthetic: a, b, v ~ N(0, 0.2^2) fp16, state ~ N(0, 1) fp32, generated on the GPU "
+                             "(seed 101234)", bound="hbm" if name == "quad-update" else "mfma")
     return build
 
 
-def extreme(args, dev):
-    """Guarded polynomial attention, B=4 S=65536 H=16 D=64; head 0 of each sample at sigma 4."""
-    from oracle.poly import poly_flops
-    from techjam_amd.implementations.poly_attention import guarded_attention
-
-    b, s, h, d = 4, 65536, 16, 64
-    g = torch.Generator(device=dev).manual_seed(1234 + 100000)
-    q = torch.randn(b, s, h, d, generator=g, device=dev) * 0.5
-    k = torch.randn(b, s, h, d, generator=g, device=dev) * 0.5
-    v = torch.randn(b, s, h, d, generator=g, device=dev)
-    q[:, :, 0] = torch.randn(b, s, d, generator=g, device=dev) * 2.0
-    k[:, :, 0] = torch.randn(b, s, d, generator=g, device=dev) * 2.0
-    qh, kh, vh = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
-    out = torch.empty(b, s, h, d, device=dev).transpose(1, 2)
-    scale = d ** -0.5
-
-    def step():
-        guarded_attention(qh, kh, vh, scale, out=out)
-
-    n_poly, n_exact = b * (h - 1), b
-    flops = n_poly * poly_flops(s, d, d, 512, 4096) + n_exact * 2.0 * d * s * (s + 1)
-    bytes_alg = 16.0 * b * s * h * d
-    config = {
-        "workload": "extreme-length attention core: guarded degree-2 polynomial attention, "
-                    "B=4 S=65536 H=16 D=64, fp32 io, 60 polynomial heads + 4 exact fallback heads",
-        "batch": b, "seq_len": s, "heads": h, "head_dim": d, "chunk": 512, "exact_prefix": 4096,
-        "data": "synthetic: q, k ~ N(0, 0.5^2), v ~ N(0, 1), head 0 of each sample q, k ~ N(0, 2^2), "
-                "generated on the GPU (seed 101234)",
-    }
-    return step, b * s, flops, bytes_alg, config, "poly_extreme_b4_s65536_h16_d64.md"
-
-
 def model(name):
-    def build(args, dev):
-        from oracle.model import DenseTransformer, generate_random_case
-        from oracle.model import TransformerConfig as OracleConfig
+    def build(args, dev) -> Workload:
         from techjam_amd.dispatcher import DispatchingTransformer
         from techjam_amd.infra import BENCHMARK_CONFIGS
+        from techjam_amd.model import TransformerConfig
 
         c = BENCHMARK_CONFIGS[name]
-        cfg = OracleConfig(c.batch_size, c.seq_len, c.d_model, c.num_heads, c.ffn_dim, c.num_layers, c.causal)
-        torch.manual_seed(1234)
-        base = DenseTransformer(cfg).eval()
-        cand = DispatchingTransformer(cfg).eval()
-        cand.load_state_dict(base.state_dict())
-        cand = cand.to(dev)
+        cfg = TransformerConfig(c.batch_size, c.seq_len, c.d_model, c.num_heads, c.ffn_dim, c.num_layers, c.causal)
+        torch.manual_seed(1234)  # default initialisation in the reference model's construction order
+        cand = DispatchingTransformer(cfg).eval().to(dev)
         cand.gemm_operands = args.gemm_operands
-        x, mask = generate_random_case(cfg, torch.device("cpu"), torch.float32, 1234 + 100000,
-                                       c.padding_ratio, 1.0)
+        x, mask = random_case(c.batch_size, c.seq_len, c.d_model, TIMING_SEED, c.padding_ratio, 1.0)
         x, mask = x.to(dev), mask.to(dev)
         lengths = mask.sum(1).tolist()
         torch.set_float32_matmul_precision(args.matmul_precision)
@@ -215,7 +302,6 @@ def model(name):
                 cand(x, mask)
 
         hd = c.d_model // c.num_heads
-        flops = c.num_layers * 2.0 * hd * c.num_heads * sum(n * (n + 1) for n in lengths)
         config = {"workload": f"{c.num_layers}-layer encoder {name}: {c.description}",
                   "batch": c.batch_size, "seq_len": c.seq_len, "d_model": c.d_model,
                   "heads": c.num_heads, "ffn_dim": c.ffn_dim, "layers": c.num_layers,
@@ -224,8 +310,97 @@ def model(name):
                           f"allow_tf32={args.allow_tf32}"
                           if args.gemm_operands == "fp32" else
                           "hipBLASLt, fp16-rounded operands (TF32 mantissa), fp32 accumulation"}
-        return step, c.batch_size * c.seq_len, flops, 0.0, config, f"model_{name.lower()}.md"
+        return Workload(step, c.batch_size * c.seq_len, c.num_layers * exact_attention_flops(lengths, c.num_heads, hd),
+                        0.0, config, f"model_{name.lower()}.md",
+                        data="synthetic: x ~ N(0, 1) with right-padded masks (seed 101234), "
+                             "default-initialised weights (seed 1234)",
+                        seeds={"timing_input": TIMING_SEED, "weights": 1234})
     return build
+
+
+# -- measurement -----------------------------------------------------------------------
+
+def timed(step, steps: int, warmup: int, dev):
+    """``steps`` launches bracketed by device synchronisations, one HIP event
+    per step boundary on the launch stream; returns (ms per step, per-step
+    ms, wall seconds of the timed region)."""
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)  # the stream the kernels are launched on
+    events = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    events[0].record(stream)
+    for i in range(steps):
+        step()
+        events[i + 1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per_step = [events[i].elapsed_time(events[i + 1]) for i in range(steps)]
+    return events[0].elapsed_time(events[-1]) / steps, per_step, wall
+
+
+def sample_stats(values: List[float]) -> dict:
+    ordered = sorted(values)
+    p90 = ordered[min(len(ordered) - 1, int(round(0.9 * (len(ordered) - 1))))]
+    return {"median": round(statistics.median(ordered), 4), "p90": round(p90, 4), "min": round(ordered[0], 4),
+            "mean": round(statistics.fmean(ordered), 4), "n": len(ordered)}
+
+
+def step_memory(step, dev) -> dict:
+    """Peak HBM allocated by torch's allocator during one step, resident inputs included."""
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(dev)
+    before = torch.cuda.memory_allocated(dev)
+    step()
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated(dev)
+    return {"peak_allocated_bytes": peak, "before_step_allocated_bytes": before,
+            "step_increment_bytes": peak - before}
+
+
+def roofline_block(w: Workload, ms: float) -> dict:
+    sec = ms / 1e3
+    tflops = w.flops / sec / 1e12
+    hbm_gbs = w.bytes_alg / sec / 1e9
+    bound = w.bound or ("mfma" if w.flops else "hbm")
+    block = {
+        "bound": "mfma",
+        "achieved": round(tflops, 2),
+        "peak": PEAK_MFMA_F16_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(tflops / PEAK_MFMA_F16_TFLOPS, 4),
+    } if bound == "mfma" else {
+        "bound": "hbm",
+        "achieved": round(hbm_gbs, 1),
+        "peak": PEAK_HBM_GBS,
+        "unit": "GB/s",
+        "frac": round(hbm_gbs / PEAK_HBM_GBS, 4),
+    }
+    block.update({
+        "traffic": traffic_from_profiles(w.profile),
+        "algorithmic_flops_per_launch": w.flops,
+        "algorithmic_bytes_per_launch": w.bytes_alg,
+        "mfma_frac_algorithmic": round(tflops / PEAK_MFMA_F16_TFLOPS, 4),
+        "hbm_frac_algorithmic": round(hbm_gbs / PEAK_HBM_GBS, 4),
+    })
+    return block
+
+
+def measure(w: Workload, args, dev) -> dict:
+    ms, per_step, wall = timed(w.step, args.steps, args.warmup, dev)
+    rec = {
+        "ms_per_step": round(ms, 4),
+        "tokens_per_s": round(w.tokens / (ms / 1e3), 1),
+        "samples_ms": sample_stats(per_step),
+        "wall_s_timed_region": round(wall, 4),
+        "roofline": roofline_block(w, ms),
+        "memory": step_memory(w.step, dev),
+    }
+    if w.accuracy is not None and not args.no_accuracy:
+        rec["accuracy"] = w.accuracy()
+    return rec
 
 
 def cpu_baseline_attn_core(repeats: int):
@@ -235,7 +410,7 @@ def cpu_baseline_attn_core(repeats: int):
     threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
     h, s, d = 16, 4096, 64
-    g = torch.Generator().manual_seed(1234 + 100000)
+    g = torch.Generator().manual_seed(TIMING_SEED)
     q, k, v = (torch.randn(1, h, s, d, generator=g) for _ in range(3))
     attn = DenseSelfAttention(h * d, h)
     with torch.inference_mode():
@@ -256,6 +431,22 @@ def cpu_baseline_attn_core(repeats: int):
     }
 
 
+def source_digest() -> str:
+    """sha256 (16 hex digits) of the kernel sources, the C header and this file."""
+    h = hashlib.sha256()
+    files = sorted((ROOT / "techjam_amd" / "csrc").glob("*")) + sorted((ROOT / "include").glob("*.h"))
+    for f in files + [Path(__file__).resolve()]:
+        h.update(f.name.encode())
+        h.update(f.read_bytes())
+    return h.hexdigest()[:16]
+
+
+BUILDERS = {"attn-core": attn_core, "extreme": extreme, "copy-1gib": copy_1gib,
+            "quad-apply": poly_part("quad-apply"), "quad-update": poly_part("quad-update"),
+            "causal-diag": poly_part("causal-diag"),
+            "model-c1": model("C1"), "model-c2": model("C2"), "model-c4": model("C4")}
+
+
 def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -268,80 +459,52 @@ def main():
     dev = torch.device("cuda:0")
     torch.backends.cuda.matmul.allow_tf32 = False
 
-    builders = {"attn-core": attn_core, "extreme": extreme, "copy-1gib": copy_1gib,
-                "quad-apply": poly_part("quad-apply"), "quad-update": poly_part("quad-update"),
-                "causal-diag": poly_part("causal-diag"),
-                "model-c1": model("C1"), "model-c2": model("C2"), "model-c4": model("C4")}
-    step, tokens, flops, bytes_alg, config, prof_name = builders[args.workload](args, dev)
-    if args.workload != "attn-core":
-        args.no_cpu_baseline = True
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-
-    stream = torch.cuda.current_stream(dev)  # the stream the kernels are launched on
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    e0.record(stream)
-    for _ in range(args.steps):
-        step()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_per_step = e0.elapsed_time(e1) / args.steps
+    w = BUILDERS[args.workload](args, dev)
+    head = measure(w, args, dev)
     gpu_state = collect_gpu_state(dev)
     noise = None
     if args.aa_reps > 0:
-        samples = time_interleaved({"step_ms": step, "step_control_ms": step}, args.aa_reps)
+        samples = time_interleaved({"step_ms": w.step, "step_control_ms": w.step}, args.aa_reps)
         stats = summarise_timings(samples, [("step_ms", "step_control_ms")])
         noise = {"samples_ms": samples, "variants": stats["variants"], **stats["noise"]}
 
-    sec = ms_per_step / 1e3
-    tflops = flops / sec / 1e12
-    hbm_gbs = bytes_alg / sec / 1e9
-    bound = config.pop("bound", "mfma" if flops else "hbm")
-    roofline = {
-        "bound": "mfma",
-        "achieved": round(tflops, 2),
-        "peak": PEAK_MFMA_F16_TFLOPS,
-        "unit": "TFLOP/s",
-        "frac": round(tflops / PEAK_MFMA_F16_TFLOPS, 4),
-    } if bound == "mfma" else {
-        "bound": "hbm",
-        "achieved": round(hbm_gbs, 1),
-        "peak": PEAK_HBM_GBS,
-        "unit": "GB/s",
-        "frac": round(hbm_gbs / PEAK_HBM_GBS, 4),
-    }
-    roofline.update({
-        "traffic": traffic_from_profiles(prof_name),
-        "algorithmic_flops_per_launch": flops,
-        "algorithmic_bytes_per_launch": bytes_alg,
-        "hbm_frac_algorithmic": round(hbm_gbs / PEAK_HBM_GBS, 4),
-    })
+    extreme_rec = None
+    if args.workload == "attn-core" and not args.no_extreme:
+        del w.step, w.accuracy  # free the attention-core tensors before allocating the next workload
+        torch.cuda.empty_cache()
+        wx = extreme(args, dev)
+        extreme_rec = {"metric": METRIC, "config": wx.config, "data": wx.data, **measure(wx, args, dev)}
+        del wx
+        torch.cuda.empty_cache()
+
     cpu = None
-    if not args.no_cpu_baseline:
+    if args.workload == "attn-core" and not args.no_cpu_baseline:
         cpu = cpu_baseline_attn_core(args.cpu_repeats)
+
     line = {
         "metric": METRIC,
-        "value": round(tokens / sec, 1),
+        "value": head["tokens_per_s"],
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16",
-        "data": config.pop("data", "synthetic: q, k, v ~ N(0, 1) generated on the GPU (seed 101234)"),
-        "config": config,
-        "roofline": roofline,
+        "data": w.data,
+        "config": w.config,
+        "roofline": head["roofline"],
         "cpu_baseline": cpu,
-        "wall_s_timed_region": round(wall, 4),
+        "samples_ms": head["samples_ms"],
+        "memory": head["memory"],
+        "accuracy": head.get("accuracy"),
+        "extreme": extreme_rec,
+        "wall_s_timed_region": head["wall_s_timed_region"],
+        "seeds": w.seeds,
+        "git": collect_git(ROOT),
+        "source_digest": source_digest(),
         "environment": collect_environment(torch, dev),
         "gpu_state": gpu_state,
     }

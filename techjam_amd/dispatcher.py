@@ -198,7 +198,6 @@ class DispatchingTransformer(TransformerEncoder):
         self._mask_ref = None
         self._mask_version = None
         self._mask_kind: Optional[MaskKind] = None
-        self._mask_lengths: Optional[torch.Tensor] = None
         self._graphs: Dict[tuple, GraphedForward] = {}
         self._graph_failures: Dict[tuple, str] = {}
 
@@ -227,7 +226,6 @@ class DispatchingTransformer(TransformerEncoder):
         self._mask_ref = None
         self._mask_version = None
         self._mask_kind = None
-        self._mask_lengths = None
 
     def _apply(self, fn, recurse: bool = True):
         result = super()._apply(fn, recurse=recurse)
@@ -252,20 +250,32 @@ class DispatchingTransformer(TransformerEncoder):
         except RuntimeError:  # inference tensors do not track versions
             return None
 
-    def _mask_info(self, mask: Optional[torch.Tensor]) -> Tuple[MaskKind, Optional[torch.Tensor]]:
-        """Kind and device int32 lengths of a mask, cached per tensor identity and version."""
-        if mask is None:
-            return MaskKind.ABSENT, None
+    def _mask_kind_cached(self, mask: torch.Tensor) -> MaskKind:
+        """Kind of a mask, classified once per tensor identity and version
+        (``src/dispatcher.py:393-423``): the classification synchronises the
+        host, so a timed loop over one mask pays it once. Inference tensors
+        carry no version counter and are treated as immutable, as there."""
         version = self._version(mask)
         cached = None if self._mask_ref is None else self._mask_ref()
         if cached is mask and version == self._mask_version and self._mask_kind is not None:
-            return self._mask_kind, self._mask_lengths
+            return self._mask_kind
         kind = classify_mask(mask)
-        lengths = mask.sum(dim=1, dtype=torch.int32) if kind is MaskKind.PREFIX else None
         self._mask_ref = weakref.ref(mask)
         self._mask_version = version
         self._mask_kind = kind
-        self._mask_lengths = lengths
+        return kind
+
+    def _mask_info(self, mask: Optional[torch.Tensor]) -> Tuple[MaskKind, Optional[torch.Tensor]]:
+        """Kind (cached) and device int32 valid lengths of a mask.
+
+        The lengths are recomputed from the live mask on every call -- one
+        asynchronous device reduction, no host synchronisation -- so a mask
+        buffer refilled in place (which an inference tensor's missing version
+        counter cannot reveal) never feeds stale lengths to the kernels."""
+        if mask is None:
+            return MaskKind.ABSENT, None
+        kind = self._mask_kind_cached(mask)
+        lengths = mask.sum(dim=1, dtype=torch.int32) if kind is MaskKind.PREFIX else None
         return kind, lengths
 
     # -- routes ------------------------------------------------------------
@@ -358,8 +368,12 @@ class DispatchingTransformer(TransformerEncoder):
 
     def _runtime_key(self, x, valid_token_mask) -> RuntimeKey:
         name, capability, arch = self._device_contract(x.device)
-        kind, _ = self._mask_info(valid_token_mask) if x.device.type == "cuda" else (
-            classify_mask(valid_token_mask), None)
+        if valid_token_mask is None:
+            kind = MaskKind.ABSENT
+        elif x.device.type == "cuda":
+            kind = self._mask_kind_cached(valid_token_mask)
+        else:
+            kind = classify_mask(valid_token_mask)
         return RuntimeKey(
             input_shape=tuple(x.shape), device_type=x.device.type, device_index=x.device.index,
             dtype=x.dtype, device_name=name, device_capability=capability, mask_kind=kind,

@@ -127,6 +127,8 @@ def scaled_dot_product_attention(
     drop it. Not combined with ``row_limit`` or ``qk_split``.
     """
     _check_qkv(q, k, v)
+    if out is not None and (out.shape != q.shape or out.dtype != q.dtype or out.device != q.device):
+        raise ValueError("out must match q in shape, dtype and device")
     dev = _require_device(q, k, v)
     b, h, s, d = q.shape
     if scale is None:

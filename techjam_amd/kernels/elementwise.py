@@ -24,6 +24,14 @@ MODE_ZERO_Y = 1      # out = x + (row valid ? y + b : 0)
 MODE_ZERO_OUT = 2    # out = row valid ? x + y + b : 0
 
 
+def _check_out(out: Optional[torch.Tensor], x: torch.Tensor) -> None:
+    """A caller-supplied ``out`` must have ``x``'s shape, dtype and device: the
+    kernels write ``x.numel()`` elements through it."""
+    if out is not None and (out.shape != x.shape or out.dtype != x.dtype or out.device != x.device):
+        raise ValueError(f"out must match x ({tuple(x.shape)}, {x.dtype}, {x.device}); "
+                         f"got ({tuple(out.shape)}, {out.dtype}, {out.device})")
+
+
 def _ok(*ts: torch.Tensor) -> bool:
     return all(t.is_cuda and t.dtype == torch.float32 and t.is_contiguous() and t.data_ptr() % 16 == 0
                and t.shape[-1] % 4 == 0 for t in ts)
@@ -37,6 +45,7 @@ def bias_residual(x: torch.Tensor, y: torch.Tensor, bias: torch.Tensor, valid_le
     if valid_len is not None and (valid_len.dtype != torch.int32 or valid_len.shape != (x.shape[0],)
                                   or valid_len.device != x.device):
         return None
+    _check_out(out, x)
     out = torch.empty_like(x) if out is None else out
     if not _ok(x, y, bias, out):
         return None
@@ -74,6 +83,7 @@ def bias_residual_layernorm(x: torch.Tensor, y: torch.Tensor, bias: torch.Tensor
     if valid_len is not None and (valid_len.dtype != torch.int32 or valid_len.shape != (x.shape[0],)
                                   or valid_len.device != x.device):
         return None
+    _check_out(out, x)
     out = torch.empty_like(x) if out is None else out
     ln = torch.empty_like(x)
     if not _ok(x, y, bias, out, ln, norm.weight, norm.bias):

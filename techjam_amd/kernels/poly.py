@@ -41,6 +41,9 @@ def poly_rows(
     Rows ``< exact_prefix`` of ``out`` are not written.
     """
     _check_qkv(q, k, v)
+    # The kernel writes B*H*S*D elements of q's type through out's strides.
+    if out is not None and (out.shape != q.shape or out.dtype != q.dtype or out.device != q.device):
+        raise ValueError("out must match q in shape, dtype and device")
     dev = _require_device(q, k, v)
     b, h, s, d = q.shape
     q, k, v = _kernel_view(q), _kernel_view(k), _kernel_view(v)

@@ -1,0 +1,68 @@
+"""Host-side argument checks and the dispatcher's mask cache (CPU).
+
+Every check here runs before any library call, so a caller's mistake is a
+Python exception rather than an out-of-bounds device write.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from techjam_amd import dispatcher as D
+from techjam_amd.implementations.attention_routing import MaskKind
+from techjam_amd.model import TransformerConfig
+
+
+def _qkv(shape=(1, 2, 64, 64), dtype=torch.float32):
+    return tuple(torch.zeros(shape, dtype=dtype) for _ in range(3))
+
+
+@pytest.mark.parametrize("bad", [(1, 2, 32, 64), (1, 2, 64, 64, "f16"), (2, 2, 64, 64)])
+def test_poly_rows_rejects_a_mismatched_out(bad):
+    from techjam_amd.kernels.poly import poly_rows
+
+    q, k, v = _qkv()
+    dtype = torch.float16 if bad[-1] == "f16" else torch.float32
+    out = torch.zeros(tuple(x for x in bad if x != "f16"), dtype=dtype)
+    with pytest.raises(ValueError, match="out must match"):
+        poly_rows(q, k, v, 0.125, torch.zeros(2, 3), out=out)
+
+
+def test_exact_attention_rejects_a_mismatched_out():
+    from techjam_amd.kernels.attention import scaled_dot_product_attention
+
+    q, k, v = _qkv()
+    for out in (torch.zeros(1, 2, 63, 64), torch.zeros(1, 2, 64, 64, dtype=torch.float16)):
+        with pytest.raises(ValueError, match="out must match"):
+            scaled_dot_product_attention(q, k, v, is_causal=True, out=out)
+
+
+def test_block_tails_reject_a_mismatched_out():
+    from techjam_amd.kernels.elementwise import MODE_PLAIN, bias_residual, bias_residual_layernorm
+
+    x, y = torch.zeros(2, 8, 256), torch.zeros(2, 8, 256)
+    bias = torch.zeros(256)
+    for out in (torch.zeros(2, 4, 256), torch.zeros(2, 8, 256, dtype=torch.float64)):
+        with pytest.raises(ValueError, match="out must match"):
+            bias_residual(x, y, bias, None, MODE_PLAIN, out=out)
+        with pytest.raises(ValueError, match="out must match"):
+            bias_residual_layernorm(x, y, bias, None, MODE_PLAIN, torch.nn.LayerNorm(256), out=out)
+
+
+def test_mask_lengths_follow_an_inference_mask_refilled_in_place():
+    """Inference tensors have no version counter: the kind stays cached, the
+    lengths must still come from the live mask on every call."""
+    cand = D.DispatchingTransformer(TransformerConfig(2, 8, 64, 1, 16, 1, True))
+    with torch.inference_mode():
+        mask = torch.zeros(2, 8, dtype=torch.bool)
+        mask[0, :5] = True
+        mask[1, :8] = True
+        kind, lengths = cand._mask_info(mask)
+        assert kind is MaskKind.PREFIX and lengths.tolist() == [5, 8]
+        mask.zero_()
+        mask[0, :2] = True
+        mask[1, :7] = True
+        kind, lengths = cand._mask_info(mask)
+        assert kind is MaskKind.PREFIX and lengths.tolist() == [2, 7]
+        assert cand._mask_info(None) == (MaskKind.ABSENT, None)
