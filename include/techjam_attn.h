@@ -13,7 +13,8 @@
  *     device memory); kernels that need scratch space take a workspace.
  *   - The return value is TJ_OK or one of the TJ_ERR_* codes below;
  *     tj_error_string() names it. Argument checks happen before any launch.
- *   - Calls are reentrant: the library keeps no mutable global state.
+ *   - Calls are reentrant: the library keeps no mutable global state, except
+ *     the fixed device scratch of tj_score_guard_noalloc (see there).
  *
  * The reference implements this path in Python on top of PyTorch SDPA and three
  * Triton kernels; each declaration names the reference interface it replaces.
@@ -38,6 +39,7 @@ extern "C" {
 #define TJ_ERR_UNSUPPORTED 4 /* valid request this build does not implement   */
 #define TJ_ERR_LAUNCH 5      /* the HIP runtime rejected a launch             */
 #define TJ_ERR_WORKSPACE 6   /* workspace missing or too small                */
+#define TJ_ERR_SCRATCH 7     /* request larger than a fixed library scratch   */
 
 /* Element types of the tensor arguments. */
 #define TJ_F32 0
@@ -151,6 +153,37 @@ int tj_score_guard(const void* q, const void* k, int dtype,
  * Workspace needed by tj_score_guard, in bytes (0 for invalid sizes).
  */
 size_t tj_score_guard_workspace_bytes(int64_t B, int64_t H, int64_t n_samples);
+
+/* Size of the fixed device scratch of tj_score_guard_noalloc, in bytes. */
+#define TJ_SCORE_GUARD_SCRATCH_BYTES ((size_t)1 << 20)
+
+/*
+ * tj_score_guard without a workspace argument and without any allocation.
+ *
+ * No counterpart in the reference. It is for callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops and
+ * harnesses that forbid hipMalloc. Same arguments (minus the workspace),
+ * checks, kernels and results (bitwise) as tj_score_guard; the per-(b,h)
+ * partial sums go to a file-scope device array of the library instead,
+ * TJ_SCORE_GUARD_SCRATCH_BYTES in size, which each device the library runs
+ * on holds until the process ends. Requests needing more than that
+ * (tj_score_guard_workspace_bytes(B, H, n_samples) > TJ_SCORE_GUARD_SCRATCH_BYTES,
+ * e.g. B*H > 5461 at 512 samples) return TJ_ERR_SCRATCH before launching.
+ * The caller still allocates the inputs and outputs. `stream` must belong to
+ * the current device (TJ_ERR_UNSUPPORTED otherwise). Every call on one device
+ * shares that device's array: calls that may overlap on one GPU (different
+ * streams, or several host threads) race and must be ordered by the caller.
+ * Nothing in the array needs to start at zero: each call writes every
+ * partial it reads.
+ */
+int tj_score_guard_noalloc(const void* q, const void* k, int dtype,
+                           int64_t B, int64_t H, int64_t S, int64_t D,
+                           const int64_t q_strides[4], const int64_t k_strides[4],
+                           float scale, const int32_t* sample_idx, int64_t n_samples,
+                           float ceiling, int64_t exact_prefix,
+                           float* sigma_out, float* mean_out, float* smax_out, int32_t* flags_out,
+                           float* coeffs_out, int32_t* row_limit_out, int32_t* split_out,
+                           hipStream_t stream);
 
 /*
  * Workspace needed by tj_poly_attn_fwd, in bytes.

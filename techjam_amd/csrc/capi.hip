@@ -12,6 +12,7 @@ extern "C" const char* tj_error_string(int code) {
     case TJ_ERR_UNSUPPORTED: return "unsupported configuration";
     case TJ_ERR_LAUNCH: return "HIP kernel launch failed";
     case TJ_ERR_WORKSPACE: return "workspace missing or too small";
+    case TJ_ERR_SCRATCH: return "request exceeds the fixed scratch of the allocation-free entry point";
     default: return "unknown error";
   }
 }

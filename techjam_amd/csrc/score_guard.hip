@@ -12,11 +12,15 @@
 // scaled), the sampled key rows stream through LDS in 64-row blocks gathered
 // with 16-byte loads, each thread forms a 4x4 tile of every 64x64 score block
 // and keeps running sum, sum of squares (fp64) and max |s|; the workgroup's
-// three partials go to the caller's workspace. The second launch (one thread
+// three partials go to a workspace -- the caller's, or for
+// tj_score_guard_noalloc a fixed array of the library. The second launch (one thread
 // per (b, h)) adds the partials of a head in a fixed order -- the result does
 // not depend on scheduling -- and writes the Bessel-corrected standard
 // deviation, the route flag and what the attention kernels read from it.
 #include <math.h>
+
+#include <atomic>
+#include <mutex>
 
 #include "tj_common.h"
 
@@ -197,14 +201,51 @@ extern "C" size_t tj_score_guard_workspace_bytes(int64_t B, int64_t H, int64_t n
   return size_t(B) * size_t(H) * size_t(tj::guard_blocks((int)n_samples)) * 3 * sizeof(double);
 }
 
-extern "C" int tj_score_guard(const void* q, const void* k, int dtype,
-                              int64_t B, int64_t H, int64_t S, int64_t D,
-                              const int64_t q_strides[4], const int64_t k_strides[4],
-                              float scale, const int32_t* sample_idx, int64_t n_samples,
-                              float ceiling, int64_t exact_prefix,
-                              float* sigma_out, float* mean_out, float* smax_out, int32_t* flags_out,
-                              float* coeffs_out, int32_t* row_limit_out, int32_t* split_out,
-                              void* workspace, size_t workspace_bytes, hipStream_t stream) {
+// Fixed scratch of tj_score_guard_noalloc: room for the partial sums of
+// B * H * ceil(n_samples / 64) workgroups (three doubles each), 1 MiB -- for
+// example 5461 (b, h) at 512 samples. Every device the library runs on holds
+// its own copy until the process ends.
+static __device__ __align__(256) double scratch[TJ_SCORE_GUARD_SCRATCH_BYTES / sizeof(double)];
+
+namespace {
+
+constexpr size_t kGuardScratchBytes = TJ_SCORE_GUARD_SCRATCH_BYTES;
+
+// Argument checks and the two launches, shared by the entry point that takes
+// a caller's workspace and the one that uses the library's fixed scratch.
+int guard_launch(const void* q, const void* k, int dtype, int64_t B, int64_t H, int64_t S, int64_t D,
+                 const int64_t q_strides[4], const int64_t k_strides[4], float scale, const int32_t* sample_idx,
+                 int64_t n_samples, float ceiling, int64_t exact_prefix, float* sigma_out, float* mean_out,
+                 float* smax_out, int32_t* flags_out, float* coeffs_out, int32_t* row_limit_out,
+                 int32_t* split_out, double* partials, hipStream_t stream) {
+  tj::GuardArgs a;
+  a.q = q; a.k = k;
+  a.vq = {q_strides[0], q_strides[1], q_strides[2]};
+  a.vk = {k_strides[0], k_strides[1], k_strides[2]};
+  a.H = (int)H; a.S = (int)S; a.D = (int)D; a.n = (int)n_samples;
+  a.scale = scale; a.ceiling = ceiling;
+  a.exact_prefix = (int)(exact_prefix < 0 ? 0 : (exact_prefix > S ? S : exact_prefix));
+  a.idx = sample_idx;
+  a.sigma = sigma_out; a.mean = mean_out; a.smax = smax_out; a.flags = flags_out; a.coeffs = coeffs_out;
+  a.row_limit = row_limit_out;
+  a.split = split_out;
+  const dim3 grid((unsigned)(B * H * tj::guard_blocks(a.n)));
+  if (dtype == TJ_F32)
+    hipLaunchKernelGGL(tj::score_guard_partial_kernel<float>, grid, dim3(tj::GT), 0, stream, a, partials);
+  else
+    hipLaunchKernelGGL(tj::score_guard_partial_kernel<half_t>, grid, dim3(tj::GT), 0, stream, a, partials);
+  const int rc = tjh::launch_status();
+  if (rc != TJ_OK) return rc;
+  const int bhn = (int)(B * H);
+  hipLaunchKernelGGL(tj::score_guard_final_kernel, dim3((unsigned)((bhn + tj::GT - 1) / tj::GT)), dim3(tj::GT), 0,
+                     stream, a, static_cast<const double*>(partials), bhn);
+  return tjh::launch_status();
+}
+
+// Checks that need no workspace; TJ_OK when the request is well formed.
+int guard_check(const void* q, const void* k, int dtype, int64_t B, int64_t H, int64_t S, int64_t D,
+                const int64_t q_strides[4], const int64_t k_strides[4], const int32_t* sample_idx,
+                int64_t n_samples, const int32_t* flags_out) {
   if (dtype != TJ_F32 && dtype != TJ_F16) return TJ_ERR_DTYPE;
   if (B <= 0 || H <= 0 || S <= 0 || D <= 0 || n_samples <= 0 || n_samples > S) return TJ_ERR_SHAPE;
   if (D > tj::GMAXD || D % 4 != 0) return TJ_ERR_UNSUPPORTED;
@@ -218,28 +259,69 @@ extern "C" int tj_score_guard(const void* q, const void* k, int dtype,
   if (B * H >= (int64_t(1) << 31) || S >= (int64_t(1) << 31)) return TJ_ERR_SHAPE;
   const size_t need = tj_score_guard_workspace_bytes(B, H, n_samples);
   if (need == 0 || B * H * tj::guard_blocks((int)n_samples) >= (int64_t(1) << 31)) return TJ_ERR_SHAPE;
-  if (workspace == nullptr || workspace_bytes < need || !tjh::aligned16(workspace)) return TJ_ERR_WORKSPACE;
-  tj::GuardArgs a;
-  a.q = q; a.k = k;
-  a.vq = {q_strides[0], q_strides[1], q_strides[2]};
-  a.vk = {k_strides[0], k_strides[1], k_strides[2]};
-  a.H = (int)H; a.S = (int)S; a.D = (int)D; a.n = (int)n_samples;
-  a.scale = scale; a.ceiling = ceiling;
-  a.exact_prefix = (int)(exact_prefix < 0 ? 0 : (exact_prefix > S ? S : exact_prefix));
-  a.idx = sample_idx;
-  a.sigma = sigma_out; a.mean = mean_out; a.smax = smax_out; a.flags = flags_out; a.coeffs = coeffs_out;
-  a.row_limit = row_limit_out;
-  a.split = split_out;
-  double* partials = static_cast<double*>(workspace);
-  const dim3 grid((unsigned)(B * H * tj::guard_blocks(a.n)));
-  if (dtype == TJ_F32)
-    hipLaunchKernelGGL(tj::score_guard_partial_kernel<float>, grid, dim3(tj::GT), 0, stream, a, partials);
-  else
-    hipLaunchKernelGGL(tj::score_guard_partial_kernel<half_t>, grid, dim3(tj::GT), 0, stream, a, partials);
-  const int rc = tjh::launch_status();
+  return TJ_OK;
+}
+
+// Device address of `scratch` per device, looked up once per device with that
+// device current. In host code the array's name is only a stand-in; kernels
+// and copies must be given this address.
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mutex;
+
+int scratch_address(hipStream_t stream, double** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return TJ_ERR_LAUNCH;
+  int stream_dev = dev;
+  if (stream != nullptr && hipStreamGetDevice(stream, &stream_dev) != hipSuccess) return TJ_ERR_LAUNCH;
+  if (stream_dev != dev) return TJ_ERR_UNSUPPORTED;  // the scratch of another device
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return TJ_ERR_LAUNCH;
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = static_cast<double*>(p);
+  return TJ_OK;
+}
+
+}  // namespace
+
+extern "C" int tj_score_guard(const void* q, const void* k, int dtype,
+                              int64_t B, int64_t H, int64_t S, int64_t D,
+                              const int64_t q_strides[4], const int64_t k_strides[4],
+                              float scale, const int32_t* sample_idx, int64_t n_samples,
+                              float ceiling, int64_t exact_prefix,
+                              float* sigma_out, float* mean_out, float* smax_out, int32_t* flags_out,
+                              float* coeffs_out, int32_t* row_limit_out, int32_t* split_out,
+                              void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  const int rc = guard_check(q, k, dtype, B, H, S, D, q_strides, k_strides, sample_idx, n_samples, flags_out);
   if (rc != TJ_OK) return rc;
-  const int bhn = (int)(B * H);
-  hipLaunchKernelGGL(tj::score_guard_final_kernel, dim3((unsigned)((bhn + tj::GT - 1) / tj::GT)), dim3(tj::GT), 0,
-                     stream, a, static_cast<const double*>(partials), bhn);
-  return tjh::launch_status();
+  const size_t need = tj_score_guard_workspace_bytes(B, H, n_samples);
+  if (workspace == nullptr || workspace_bytes < need || !tjh::aligned16(workspace)) return TJ_ERR_WORKSPACE;
+  return guard_launch(q, k, dtype, B, H, S, D, q_strides, k_strides, scale, sample_idx, n_samples, ceiling,
+                      exact_prefix, sigma_out, mean_out, smax_out, flags_out, coeffs_out, row_limit_out, split_out,
+                      static_cast<double*>(workspace), stream);
+}
+
+extern "C" int tj_score_guard_noalloc(const void* q, const void* k, int dtype,
+                                      int64_t B, int64_t H, int64_t S, int64_t D,
+                                      const int64_t q_strides[4], const int64_t k_strides[4],
+                                      float scale, const int32_t* sample_idx, int64_t n_samples,
+                                      float ceiling, int64_t exact_prefix,
+                                      float* sigma_out, float* mean_out, float* smax_out, int32_t* flags_out,
+                                      float* coeffs_out, int32_t* row_limit_out, int32_t* split_out,
+                                      hipStream_t stream) {
+  const int rc = guard_check(q, k, dtype, B, H, S, D, q_strides, k_strides, sample_idx, n_samples, flags_out);
+  if (rc != TJ_OK) return rc;
+  if (tj_score_guard_workspace_bytes(B, H, n_samples) > kGuardScratchBytes) return TJ_ERR_SCRATCH;
+  double* partials = nullptr;
+  const int src = scratch_address(stream, &partials);
+  if (src != TJ_OK) return src;
+  return guard_launch(q, k, dtype, B, H, S, D, q_strides, k_strides, scale, sample_idx, n_samples, ceiling,
+                      exact_prefix, sigma_out, mean_out, smax_out, flags_out, coeffs_out, row_limit_out, split_out,
+                      partials, stream);
 }

@@ -22,6 +22,7 @@ TJ_ERR_ALIGN = 3
 TJ_ERR_UNSUPPORTED = 4
 TJ_ERR_LAUNCH = 5
 TJ_ERR_WORKSPACE = 6
+TJ_ERR_SCRATCH = 7
 
 TJ_F32 = 0
 TJ_F16 = 1
@@ -50,6 +51,11 @@ SIGNATURES = {
         _int,
         [_vp, _vp, _int, _i64, _i64, _i64, _i64, _i64p, _i64p, _f32, _vp, _i64, _f32, _i64,
          _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp],
+    ),
+    "tj_score_guard_noalloc": (
+        _int,
+        [_vp, _vp, _int, _i64, _i64, _i64, _i64, _i64p, _i64p, _f32, _vp, _i64, _f32, _i64,
+         _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     ),
     "tj_score_guard_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64]),
     "tj_poly_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, _i64]),
@@ -124,7 +130,7 @@ def check(code: int, what: str) -> None:
     if code == TJ_OK:
         return
     msg = f"{what}: {error_text(code)} (code {code})"
-    if code in (TJ_ERR_SHAPE, TJ_ERR_DTYPE, TJ_ERR_ALIGN, TJ_ERR_WORKSPACE):
+    if code in (TJ_ERR_SHAPE, TJ_ERR_DTYPE, TJ_ERR_ALIGN, TJ_ERR_WORKSPACE, TJ_ERR_SCRATCH):
         raise ValueError(msg)
     if code == TJ_ERR_UNSUPPORTED:
         raise UnsupportedCaseError(msg)

@@ -42,8 +42,8 @@ def test_library_exports_every_declared_symbol():
 def test_error_strings_are_distinct_and_never_null():
     from techjam_amd.kernels import _lib
 
-    texts = {_lib.error_text(c) for c in range(0, 7)}
-    assert len(texts) == 7
+    texts = {_lib.error_text(c) for c in range(0, 8)}
+    assert len(texts) == 8
     assert _lib.error_text(12345) == "unknown error"
 
 
@@ -209,3 +209,27 @@ def test_block_tails_reject_bad_arguments_before_launching():
     assert L.tj_bias_gelu(16, 16, 4, 6, None) == _lib.TJ_ERR_UNSUPPORTED
     assert L.tj_bias_gelu(8, 16, 4, 8, None) == _lib.TJ_ERR_ALIGN
     assert L.tj_bias_gelu(16, 16, -1, 8, None) == _lib.TJ_ERR_SHAPE
+
+
+def test_noalloc_guard_rejects_requests_beyond_its_scratch_before_launching():
+    """tj_score_guard_noalloc checks its arguments, then the size of its fixed
+    scratch, before any HIP call (so these run without a GPU)."""
+    from techjam_amd.kernels import _lib
+
+    L = _lib.lib()
+    f = L.tj_score_guard_noalloc
+    st = _strides(16 * 4096 * 64, 4096 * 64, 64, 1)
+    outs = [16] * 7
+    # 6000 (b, h) x 8 row blocks x 24 bytes = 1.15 MB > 1 MiB
+    assert f(16, 16, _lib.TJ_F32, 375, 16, 4096, 64, st, st, 0.125, 16, 512, 0.4, 4096, *outs, None) == \
+        _lib.TJ_ERR_SCRATCH
+    assert f(16, 16, 9, 1, 16, 4096, 64, st, st, 0.125, 16, 512, 0.4, 4096, *outs, None) == _lib.TJ_ERR_DTYPE
+    assert f(16, 16, _lib.TJ_F32, 1, 16, 100, 64, st, st, 0.125, 16, 512, 0.4, 4096, *outs, None) == \
+        _lib.TJ_ERR_SHAPE  # more samples than rows
+    assert f(16, 16, _lib.TJ_F32, 1, 16, 4096, 66, st, st, 0.125, 16, 512, 0.4, 4096, *outs, None) == \
+        _lib.TJ_ERR_UNSUPPORTED
+    # the same request through the workspace entry point is limited only by its workspace
+    g = L.tj_score_guard
+    assert g(16, 16, _lib.TJ_F32, 375, 16, 4096, 64, st, st, 0.125, 16, 512, 0.4, 4096, *outs, None, 0, None) == \
+        _lib.TJ_ERR_WORKSPACE
+    assert L.tj_score_guard_workspace_bytes(5461, 1, 512) <= 1 << 20 < L.tj_score_guard_workspace_bytes(5462, 1, 512)
