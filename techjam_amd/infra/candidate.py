@@ -1,13 +1,18 @@
 """Candidate contract consumed by a benchmark harness.
 
-Same fields and refusal rules as the reference's ``src/infra/candidate.py:15-232``
-(a harness written against it loads this package's ``CANDIDATE`` unchanged);
+Same fields and refusal rules as the reference's ``src/infra/candidate.py:15-232``;
 the only generalisation is that device constraints are phrased for any GPU
 runtime torch exposes as ``"cuda"`` -- ROCm here.
+
+The reference's ``load_candidate`` accepts only instances of *its own*
+``CandidateSpec`` class (``src/infra/candidate.py:156``), so this package's
+``CANDIDATE`` reaches a reference harness through ``as_spec``: a module on the
+reference side builds the reference's class from this one's fields.
 """
 
 from __future__ import annotations
 
+import dataclasses
 import importlib
 import re
 from dataclasses import dataclass
@@ -93,6 +98,20 @@ class CandidateSpec:
                     and all(isinstance(v, str) and v for v in versions)):
                 raise TypeError("version contracts require non-empty version strings")
             seen.add(case_id)
+
+
+def as_spec(spec_class, candidate: CandidateSpec):
+    """``candidate`` rebuilt as an instance of another ``CandidateSpec`` class
+    with the same fields -- the reference's, so that its ``load_candidate``
+    type check passes. Values are passed as they are (the model factory stays
+    this package's ``DispatchingTransformer``); a field the target class lacks,
+    or one it requires that this class does not have, is an error."""
+    ours = {f.name for f in dataclasses.fields(CandidateSpec)}
+    theirs = {f.name for f in dataclasses.fields(spec_class)}
+    if ours != theirs:
+        raise TypeError(f"{spec_class.__qualname__} fields differ from the candidate contract: "
+                        f"missing {sorted(ours - theirs)}, extra {sorted(theirs - ours)}")
+    return spec_class(**{name: getattr(candidate, name) for name in sorted(ours)})
 
 
 def load_candidate(selector: str) -> CandidateSpec:

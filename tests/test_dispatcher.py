@@ -332,3 +332,43 @@ def test_candidate_spec_validation_rules():
         CandidateSpec("ok", D.DispatchingTransformer, "o", "d", unsupported_official_cases=(15,)).validate()
     with pytest.raises(ValueError):
         CandidateSpec("ok", D.DispatchingTransformer, "o", "d", official_case_dtypes=((1, ("int8",)),)).validate()
+
+
+# The reference's CandidateSpec field list (src/infra/candidate.py:15-39), in
+# declaration order, restated as the interface a harness binds to.
+REFERENCE_CANDIDATE_FIELDS = (
+    "name", "model_factory", "owner", "description", "weight_loader", "strict_weight_copy",
+    "self_compiling", "unsupported_official_cases", "official_case_dtypes", "candidate_only_official_cases",
+    "default_input_scale_only_cases", "cuda_only_official_cases", "official_case_min_cuda_capability",
+    "official_case_torch_versions",
+)
+
+
+def test_candidate_fields_are_the_reference_contract():
+    import dataclasses
+
+    assert tuple(f.name for f in dataclasses.fields(D.CANDIDATE)) == REFERENCE_CANDIDATE_FIELDS
+
+
+def test_candidate_converts_to_a_foreign_spec_class():
+    """What the reference-side module does: build the reference's own class
+    (here a stand-in with the same field list and defaults) from CANDIDATE,
+    both through ``as_spec`` and through ``dataclasses.asdict``."""
+    import dataclasses
+
+    from techjam_amd.infra import as_spec
+
+    defaults = {f.name: f for f in dataclasses.fields(D.CANDIDATE)}
+    Foreign = dataclasses.make_dataclass(
+        "CandidateSpec",
+        [(n, object) if defaults[n].default is dataclasses.MISSING else (n, object, dataclasses.field(
+            default=defaults[n].default)) for n in REFERENCE_CANDIDATE_FIELDS],
+        frozen=True)
+    for spec in (as_spec(Foreign, D.CANDIDATE), Foreign(**dataclasses.asdict(D.CANDIDATE))):
+        assert type(spec) is Foreign
+        for name in REFERENCE_CANDIDATE_FIELDS:
+            assert getattr(spec, name) == getattr(D.CANDIDATE, name), name
+        assert spec.model_factory is D.DispatchingTransformer
+    Short = dataclasses.make_dataclass("Short", [("name", str)], frozen=True)
+    with pytest.raises(TypeError, match="fields differ"):
+        as_spec(Short, D.CANDIDATE)
