@@ -323,6 +323,7 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
         }
 
       half8_t pf[QB][4];
+      float shift[QB];
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
         const int qb0 = qw0 + 32 * qb;
@@ -348,10 +349,18 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
         // Lazy rescaling: the reference point moves only when a row's max grows
         // by more than 2^8 (p <= 256 is exact enough in fp16 and harmless in the
         // fp32 accumulators); the first tile always sets it.
-        const float shift = first ? t_max : (t_max > kRescaleLog2 ? t_max : 0.f);
-        if (first || __any(shift != 0.f)) {
-          const float alpha = first ? 0.f : fast_exp2(-shift);
-          m_run[qb] = first ? shift : m_run[qb] + shift;
+        shift[qb] = first ? t_max : (t_max > kRescaleLog2 ? t_max : 0.f);
+      }
+      // One wave-wide decision per tile for all query blocks (a lane or block
+      // whose shift is 0 rescales by exactly 1).
+      bool moved = false;
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) moved |= shift[qb] != 0.f;
+      if (first || __any(moved)) {
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          const float alpha = first ? 0.f : fast_exp2(-shift[qb]);
+          m_run[qb] = first ? shift[qb] : m_run[qb] + shift[qb];
           l_run[qb] *= alpha;
 #pragma unroll
           for (int db = 0; db < TL::DB; ++db)
@@ -360,11 +369,15 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
 #pragma unroll
           for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) sacc[qb][kb][r] -= shift;
+            for (int r = 0; r < 16; ++r) sacc[qb][kb][r] -= shift[qb];
 #pragma unroll
           for (int r = 0; r < 16; ++r) cneg[qb][r] = -m_run[qb];
         }
-        // P = exp2(S) rounded to fp16; the row sum adds the same rounded values.
+      }
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        // P = exp2(S) rounded to fp16; the row sum adds the same rounded
+        // values (a dominant key's rounding then cancels in the normalisation).
 #pragma unroll
         for (int s = 0; s < 4; ++s)
 #pragma unroll

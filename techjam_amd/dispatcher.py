@@ -23,7 +23,9 @@ Keeps the public interface of the reference's ``src/dispatcher.py:39-818`` --
 * official case 6 streams batch slices (``:452-465``); official case 14 streams
   trimmed prefixes through the guarded polynomial module (``:488-538``), with
   its FP32 interface computed in FP32 around fp16-MFMA attention instead of
-  casting the model to FP16.
+  casting the model to FP16. Their chunk sizes come from the streaming
+  planner (``implementations.planner``), which budgets the HIP path's real
+  working set instead of the reference's SDPA score-copy estimate.
 """
 
 from __future__ import annotations
@@ -40,10 +42,10 @@ from .implementations.attention_routing import MaskKind, classify_mask
 from .implementations.extreme import (
     CASE_14_CONFIG,
     PolyOrExactSelfAttention,
-    choose_batch_chunk_size,
     forward_batch_chunks,
     forward_prefix_chunks,
 )
+from .implementations.planner import ChunkPlan, plan_for_input
 from .implementations.sdpa import PackedQKVSDPASelfAttention, StridedSDPASelfAttention
 from .infra import BENCHMARK_CONFIGS, CandidateSpec, OfficialCase, load_official_cases
 from .kernels.attention import SUPPORTED_HEAD_DIMS, kernel_head_dim
@@ -178,6 +180,9 @@ class DispatchingTransformer(TransformerEncoder):
     #: ``GRAPH_MAX_TOKENS`` tokens (inference only); ``TECHJAM_AMD_GRAPHS=0``
     #: in the environment turns it off.
     use_graphs = True
+    #: Device bytes the streamed routes (cases 6 and 14) may plan for; None
+    #: takes 85 % of the device less what is already allocated.
+    memory_budget_bytes: Optional[int] = None
 
     def __init__(self, config: TransformerConfig) -> None:
         super().__init__(config)
@@ -195,6 +200,7 @@ class DispatchingTransformer(TransformerEncoder):
         self._device_contracts: Dict[tuple, tuple] = {}
         self._last_route: Optional[RouteDecision] = None
         self._last_extreme_chunk_size: Optional[int] = None
+        self._last_chunk_plan: Optional[ChunkPlan] = None
         self._mask_ref = None
         self._mask_version = None
         self._mask_kind: Optional[MaskKind] = None
@@ -215,6 +221,11 @@ class DispatchingTransformer(TransformerEncoder):
     def last_extreme_chunk_size(self) -> Optional[int]:
         return self._last_extreme_chunk_size
 
+    @property
+    def last_chunk_plan(self) -> Optional[ChunkPlan]:
+        """The streaming planner's decision for the last streamed forward."""
+        return self._last_chunk_plan
+
     def clear_runtime_cache(self) -> None:
         self._graphs.clear()
         self._graph_failures.clear()
@@ -223,6 +234,7 @@ class DispatchingTransformer(TransformerEncoder):
         self._device_contracts.clear()
         self._last_route = None
         self._last_extreme_chunk_size = None
+        self._last_chunk_plan = None
         self._mask_ref = None
         self._mask_version = None
         self._mask_kind = None
@@ -315,9 +327,15 @@ class DispatchingTransformer(TransformerEncoder):
             self._graphs[key] = graphed
         return graphed(x, mask, lengths)
 
+    def _plan_chunk(self, x, poly: bool) -> int:
+        plan = plan_for_input(x, self.config.num_heads, self.config.ffn_dim, poly=poly,
+                              budget_bytes=self.memory_budget_bytes)
+        self._last_chunk_plan = plan
+        self._last_extreme_chunk_size = plan.chunk
+        return plan.chunk
+
     def _forward_case_6(self, x, valid_token_mask=None):
-        chunk = choose_batch_chunk_size(x, self.config.num_heads, score_copies=0, activation_copies=12)
-        self._last_extreme_chunk_size = chunk
+        chunk = self._plan_chunk(x, poly=False)
         return forward_batch_chunks(self._forward_hip_chunk, x, valid_token_mask, chunk)
 
     def _forward_hip_chunk(self, x, valid_token_mask=None):
@@ -334,8 +352,7 @@ class DispatchingTransformer(TransformerEncoder):
         return self.forward_layers(x, None, None)
 
     def _forward_case_14(self, x, valid_token_mask=None):
-        chunk = choose_batch_chunk_size(x, self.config.num_heads, score_copies=0, activation_copies=12)
-        self._last_extreme_chunk_size = chunk
+        chunk = self._plan_chunk(x, poly=True)
         return forward_prefix_chunks(self._forward_case_14_chunk, x, valid_token_mask, chunk)
 
     def forward_case14_streamed_sample(self, x, valid_token_mask=None):

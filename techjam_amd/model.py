@@ -223,13 +223,21 @@ class EncoderBlock(nn.Module):
         y = _linear_f32(h, self.ffn_out.weight)
         return _must(bias_residual(x, y, self.ffn_out.bias, valid_len, MODE_ZERO_OUT, out=y))
 
-    def _forward_fused_norms(self, x, xn, valid_token_mask, causal, valid_len, next_norm, last,
+    def _forward_fused_norms(self, state, valid_token_mask, causal, valid_len, next_norm, last,
                              fp16_operands=False):
-        """``_forward_fused`` that takes ``norm1(x)`` ready-made and hands back
+        """``_forward_fused`` that takes ``state = [x, norm1(x)]`` and hands back
         ``(x_out, next_norm(x_out))``: each residual pass also writes the
         LayerNorm its result feeds (``norm2`` here, then the next block's
         ``norm1`` or the final norm, with padded rows zeroed after the last
         block).
+
+        ``state`` is emptied on entry, so this method holds the only
+        references to its inputs and every intermediate is released at its
+        last use: the largest set alive at once is the residual, the normed
+        input, q/k/v and the attention output during attention, and the
+        residual, one normed copy and the FFN hidden activation afterwards --
+        the working set the streaming planner
+        (``implementations.planner``) budgets for.
 
         ``fp16_operands`` rounds every GEMM input (normed activations, the
         attention output, the GELU output, weights) to fp16 -- the 10-bit
@@ -241,12 +249,23 @@ class EncoderBlock(nn.Module):
 
         attn = self.attention
         f32 = torch.float32
-        ctx = attn.context(xn.half() if fp16_operands else xn, valid_token_mask, causal, valid_len)
+        x, a = state
+        state.clear()
+        if fp16_operands:
+            a = a.half()
+        ctx = attn.context(a, valid_token_mask, causal, valid_len)
+        del a
         y = project(ctx, attn.out_proj.weight, attn.out_proj, "weight", f32)
-        x, xn2 = _must(bias_residual_layernorm(x, y, attn.out_proj.bias, valid_len, MODE_ZERO_Y, self.norm2, out=y))
-        h = project(xn2.half() if fp16_operands else xn2, self.ffn_in.weight, self.ffn_in, "weight", f32)
+        del ctx
+        x, a = _must(bias_residual_layernorm(x, y, attn.out_proj.bias, valid_len, MODE_ZERO_Y, self.norm2, out=y))
+        del y
+        if fp16_operands:
+            a = a.half()
+        h = project(a, self.ffn_in.weight, self.ffn_in, "weight", f32)
+        del a
         _must(bias_gelu(h, self.ffn_in.bias))
         y = project(h.half() if fp16_operands else h, self.ffn_out.weight, self.ffn_out, "weight", f32)
+        del h
         return _must(bias_residual_layernorm(x, y, self.ffn_out.bias, valid_len, MODE_ZERO_OUT, next_norm, out=y,
                                              zero_padded_norm=last and valid_token_mask is not None))
 
@@ -301,13 +320,14 @@ class TransformerEncoder(nn.Module):
     def _forward_layers_fused(self, x, valid_token_mask, valid_len):
         """The layer stack with every LayerNorm but the first fused into the
         residual pass before it (same computation as the loop above)."""
-        xn = self.layers[0].norm1(x)
+        state = [x, self.layers[0].norm1(x)]
+        del x
         n = len(self.layers)
         for i, layer in enumerate(self.layers):
             nxt = self.layers[i + 1].norm1 if i + 1 < n else self.final_norm
-            x, xn = layer._forward_fused_norms(x, xn, valid_token_mask, self.config.causal, valid_len, nxt,
-                                               last=i + 1 == n, fp16_operands=self.gemm_operands == "fp16")
-        return xn
+            state = list(layer._forward_fused_norms(state, valid_token_mask, self.config.causal, valid_len, nxt,
+                                                    last=i + 1 == n, fp16_operands=self.gemm_operands == "fp16"))
+        return state[1]
 
     def forward(self, x, valid_token_mask: Optional[torch.Tensor] = None):
         valid_len = None if valid_token_mask is None else prefix_lengths(valid_token_mask)

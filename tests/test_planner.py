@@ -1,0 +1,69 @@
+"""Streaming planner known answers (CPU; the library is loaded for its
+workspace-size queries, no kernel runs)."""
+
+from __future__ import annotations
+
+import pytest
+
+from techjam_amd.implementations import planner as P
+
+MIB = 1 << 20
+
+
+def test_workspace_sizes_come_from_the_library():
+    ws = P.poly_workspace_bytes_per_head()
+    # fp32 masters (S_quad 64x64x64 = 1 MiB and the small states), a 16-slot
+    # ring of fp16 shadows (~0.5 MiB each) and two launches of fp16 token images
+    assert 10 * MIB < ws < 13 * MIB
+    assert P.guard_workspace_bytes_per_head() == 8 * 3 * 8  # 512 samples = 8 row blocks x 3 doubles
+
+
+def test_case_6_known_answers():
+    """Case 6: B=10000, S=128, d_model=128, H=4, FFN=128."""
+    fp = P.encoder_item_footprint(128, 128, 4, 128)
+    act = 128 * 128 * 4
+    assert fp.per_item_bytes == 6 * act and fp.output_per_item_bytes == act
+    plan = P.plan_batch_chunk(10000, fp, 24 << 30)
+    assert plan.chunk == 8192
+    assert plan.reserved_bytes == 10000 * act + P.LIBRARY_ALLOWANCE_BYTES
+    # a 1 GiB budget: (2^30 - 655,360,000 - 2^28) // 393,216 = 381 -> 256
+    assert P.plan_batch_chunk(10000, fp, 1 << 30).chunk == 256
+    assert P.plan_batch_chunk(10000, fp, 0).chunk == 1
+
+
+def test_case_14_known_answers():
+    """Case 14: B=32, S=100000, d_model=1024, H=16, FFN=1024, guarded polynomial route."""
+    fp = P.encoder_item_footprint(100000, 1024, 16, 1024, poly=True)
+    act = 100000 * 1024 * 4
+    ws = 16 * (P.poly_workspace_bytes_per_head() + P.guard_workspace_bytes_per_head()
+               + P.GUARD_OUTPUT_BYTES_PER_HEAD)
+    assert fp.per_item_bytes == 6 * act + ws
+    # the reference's RTX 5080 budget (23,034 MiB) gives its own answer, 4
+    assert P.plan_batch_chunk(32, fp, 23_034 * MIB).chunk == 4
+    # 85 % of an MI355X's 288 GB holds the whole batch
+    assert P.plan_batch_chunk(32, fp, int(0.85 * 288e9)).chunk == 32
+    # fp16 activations halve the activation part, not the workspaces
+    fp16 = P.encoder_item_footprint(100000, 1024, 16, 1024, poly=True, element_size=2)
+    assert fp16.per_item_bytes == 6 * act // 2 + ws
+
+
+def test_extreme_attention_core_fits_8_gib():
+    """B=4, S=65536, H=16, D=64 guarded attention: output, workspaces and the
+    resident fp32 q, k, v stay under 8 GiB."""
+    inputs = 3 * 4 * 65536 * 16 * 64 * 4
+    total = inputs + P.attention_core_bytes(4, 16, 65536, 64, poly=True)
+    assert total < 8 << 30
+    assert P.attention_core_bytes(4, 16, 65536, 64, poly=False) == 1 << 30
+
+
+def test_ffn_phase_dominates_wide_ffns():
+    fp = P.encoder_item_footprint(8192, 1024, 16, 8192)
+    act, hidden = 8192 * 1024 * 4, 8192 * 8192 * 4
+    assert fp.per_item_bytes == act + 2 * hidden
+
+
+def test_rejects_bad_sizes():
+    with pytest.raises(ValueError):
+        P.encoder_item_footprint(0, 128, 4, 128)
+    with pytest.raises(ValueError):
+        P.plan_batch_chunk(0, P.encoder_item_footprint(8, 8, 1, 8), 1 << 20)
