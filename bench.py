@@ -76,6 +76,8 @@ def parse_args():
     p.add_argument("--no-extreme", action="store_true",
                    help="with the default workload, skip the extreme-length measurement")
     p.add_argument("--no-accuracy", action="store_true", help="skip the sampled-heads accuracy check")
+    p.add_argument("--no-models", action="store_true",
+                   help="with the default workload, skip the C2/C4 encoder timings on both GEMM-operand paths")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-repeats", type=int, default=3)
     p.add_argument("--aa-reps", type=int, default=0,
@@ -301,6 +303,10 @@ def model(name):
             with torch.inference_mode():
                 cand(x, mask)
 
+        def outputs():
+            with torch.inference_mode():
+                return cand(x, mask)
+
         hd = c.d_model // c.num_heads
         config = {"workload": f"{c.num_layers}-layer encoder {name}: {c.description}",
                   "batch": c.batch_size, "seq_len": c.seq_len, "d_model": c.d_model,
@@ -310,12 +316,21 @@ def model(name):
                           f"allow_tf32={args.allow_tf32}"
                           if args.gemm_operands == "fp32" else
                           "hipBLASLt, fp16-rounded operands (TF32 mantissa), fp32 accumulation"}
-        return Workload(step, c.batch_size * c.seq_len, c.num_layers * exact_attention_flops(lengths, c.num_heads, hd),
-                        0.0, config, f"model_{name.lower()}.md",
-                        data="synthetic: x ~ N(0, 1) with right-padded masks (seed 101234), "
-                             "default-initialised weights (seed 1234)",
-                        seeds={"timing_input": TIMING_SEED, "weights": 1234})
+        w = Workload(step, c.batch_size * c.seq_len, c.num_layers * exact_attention_flops(lengths, c.num_heads, hd),
+                     0.0, config, f"model_{name.lower()}.md",
+                     data="synthetic: x ~ N(0, 1) with right-padded masks (seed 101234), "
+                          "default-initialised weights (seed 1234)",
+                     seeds={"timing_input": TIMING_SEED, "weights": 1234})
+        w.outputs = outputs
+        return w
+    build.__doc__ = BENCHMARK_CONFIG_TEXT.get(name)
     return build
+
+
+BENCHMARK_CONFIG_TEXT = {
+    "C2": "4-layer encoder, B=8 S=1024 d_model=512 H=8 FFN=2048, packed QKV, causal, right padding",
+    "C4": "4-layer encoder, B=2 S=8192 d_model=1024 H=16 FFN=4096, causal, right padding",
+}
 
 
 # -- measurement -----------------------------------------------------------------------
@@ -403,6 +418,30 @@ def measure(w: Workload, args, dev) -> dict:
     return rec
 
 
+def encoder_operand_paths(name: str, args, dev) -> dict:
+    """One encoder (C2 or C4) timed on both GEMM-operand paths, same weights
+    and inputs: float32 GEMMs under the harness flags, and fp16 operands with
+    fp32 accumulation. ``max_abs_between_paths`` is how far the fp16 path's
+    output moves from the float32 path's (the oracle comparison itself is in
+    the tests)."""
+    rec = {}
+    outs = {}
+    for operands in ("fp32", "fp16"):
+        args.gemm_operands = operands
+        w = model(name)(args, dev)
+        ms, per_step, _ = timed(w.step, args.steps, args.warmup, dev)
+        rec[operands] = {"ms_per_step": round(ms, 4), "tokens_per_s": round(w.tokens / (ms / 1e3), 1),
+                         "samples_ms": sample_stats(per_step), "gemm": w.config["gemm"]}
+        outs[operands] = w.outputs()
+        del w
+    rec["max_abs_between_paths"] = float((outs["fp16"] - outs["fp32"]).abs().max())
+    rec["workload"] = f"{name}: {model(name).__doc__ or ''}".strip()
+    args.gemm_operands = "fp32"
+    torch.set_float32_matmul_precision("highest")  # the model builder set the harness flags
+    torch.backends.cuda.matmul.allow_tf32 = False
+    return rec
+
+
 def cpu_baseline_attn_core(repeats: int):
     """Dense FP32 oracle attention on the host: one batch element (16 heads x 4096)."""
     from oracle.model import DenseSelfAttention
@@ -477,6 +516,11 @@ def main():
         del wx
         torch.cuda.empty_cache()
 
+    models_rec = None
+    if args.workload == "attn-core" and not args.no_models:
+        models_rec = {name: encoder_operand_paths(name, args, dev) for name in ("C2", "C4")}
+        torch.cuda.empty_cache()
+
     cpu = None
     if args.workload == "attn-core" and not args.no_cpu_baseline:
         cpu = cpu_baseline_attn_core(args.cpu_repeats)
@@ -501,6 +545,7 @@ def main():
         "memory": head["memory"],
         "accuracy": head.get("accuracy"),
         "extreme": extreme_rec,
+        "encoders": models_rec,
         "wall_s_timed_region": head["wall_s_timed_region"],
         "seeds": w.seeds,
         "git": collect_git(ROOT),

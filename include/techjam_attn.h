@@ -276,10 +276,16 @@ int tj_bias_residual(float* out, const float* x, const float* y, const float* bi
                      int mode, hipStream_t stream);
 
 /*
- * y = gelu(y + bias) in place, exact (erf) GELU -- the bias of the FFN input
- * GEMM fused with F.gelu(approximate="none") (torch_transformer_benchmark.py:145).
+ * gelu(y + bias), exact (erf) GELU -- the bias of the FFN input GEMM fused
+ * with F.gelu(approximate="none") (torch_transformer_benchmark.py:145).
+ * out_f16 == NULL: y is overwritten with the result (fp32). Otherwise the
+ * result is written, rounded to fp16, to out_f16 ([rows, cols], 8-byte
+ * aligned, not overlapping y) and y is left unchanged: the fp16 operand of
+ * the FFN output GEMM when the encoder's GEMMs take fp16 operands (the fused
+ * cast of the packed-projection path, src/implementations/sdpa.py:127-138,
+ * applied to the block's other GEMM inputs).
  */
-int tj_bias_gelu(float* y, const float* bias, int64_t rows, int64_t cols, hipStream_t stream);
+int tj_bias_gelu(float* y, const float* bias, int64_t rows, int64_t cols, void* out_f16, hipStream_t stream);
 
 /*
  * tj_bias_residual (same modes, out may alias x or y) fused with the
@@ -287,12 +293,14 @@ int tj_bias_gelu(float* y, const float* bias, int64_t rows, int64_t cols, hipStr
  * norm2 after the attention residual, the next block's norm1 or the final norm
  * after the FFN residual, :163-172):
  *   ln_out[r,:] = (out[r,:] - mean) / sqrt(var + eps) * gamma + beta,
- * mean and biased variance over the row, as torch.nn.LayerNorm defines them.
+ * mean and biased variance over the row, as torch.nn.LayerNorm defines them,
+ * stored as ln_dtype (TJ_F32, or TJ_F16 when the norm feeds a GEMM with fp16
+ * operands; the statistics are fp32 either way).
  * With zero_ln_padded, rows at or past valid_len get ln_out = 0 (the final
  * masked_fill). ln_out must not overlap out. cols must be 256, 512, 1024 or
  * 2048 (TJ_ERR_UNSUPPORTED otherwise); all pointers 16-byte aligned.
  */
-int tj_bias_residual_layernorm(float* out, float* ln_out, const float* x, const float* y,
+int tj_bias_residual_layernorm(float* out, void* ln_out, int ln_dtype, const float* x, const float* y,
                                const float* bias, const float* gamma, const float* beta,
                                int64_t rows, int64_t cols, int64_t seq_len,
                                const int32_t* valid_len, int mode, float eps,

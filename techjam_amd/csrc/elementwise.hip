@@ -6,11 +6,13 @@
 //   tj_bias_residual : out = x + (row valid ? y + b : 0)          (mode 1)
 //                      out = row valid ? x + y + b : 0             (mode 2)
 //                      out = x + y + b                             (mode 0)
-//   tj_bias_gelu     : y = gelu(y + b), exact (erf) form, in place
+//   tj_bias_gelu     : y = gelu(y + b), exact (erf) form, in place -- or
+//                      written as fp16 to a separate buffer, the operand of
+//                      the next GEMM when GEMMs take fp16 operands
 //   tj_bias_residual_layernorm : one of the residual forms above, and in the
 //                      same pass n = LayerNorm(out) (the next block's norm, or
 //                      the final one), so that the norm does not read the
-//                      residual stream again
+//                      residual stream again; n in fp32 or fp16
 //
 // Tensors are fp32 [rows, cols] row-major with cols % 4 == 0 and 16-byte
 // aligned bases; row r = b * seq_len + s is valid iff s < valid_len[b].
@@ -25,6 +27,12 @@ __device__ __forceinline__ bool row_valid(int64_t row, int64_t seq_len, const in
   if (valid_len == nullptr) return true;
   const int64_t b = row / seq_len, s = row % seq_len;
   return s < (int64_t)valid_len[b];
+}
+
+// Four consecutive values to element 4i of an fp32 or fp16 array.
+__device__ __forceinline__ void store4(float* p, int64_t i, float4_t v) { reinterpret_cast<float4_t*>(p)[i] = v; }
+__device__ __forceinline__ void store4(half_t* p, int64_t i, float4_t v) {
+  reinterpret_cast<half4_t*>(p)[i] = half4_t{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
 }
 
 __global__ __launch_bounds__(ET) void bias_residual_kernel(float* out, const float* x, const float* y, const float* bias,
@@ -46,7 +54,8 @@ __global__ __launch_bounds__(ET) void bias_residual_kernel(float* out, const flo
   }
 }
 
-__global__ __launch_bounds__(ET) void bias_gelu_kernel(float* y, const float* bias, int64_t n4, int64_t c4) {
+template <typename TO>
+__global__ __launch_bounds__(ET) void bias_gelu_kernel(float* y, TO* out, const float* bias, int64_t n4, int64_t c4) {
   for (int64_t i = blockIdx.x * (int64_t)ET + threadIdx.x; i < n4; i += (int64_t)gridDim.x * ET) {
     const int64_t c = i % c4;
     float4_t v = reinterpret_cast<const float4_t*>(y)[i];
@@ -56,7 +65,7 @@ __global__ __launch_bounds__(ET) void bias_gelu_kernel(float* y, const float* bi
       const float t = v[e] + bv[e];
       v[e] = 0.5f * t * (1.f + erff(t * 0.70710678118654752f));
     }
-    reinterpret_cast<float4_t*>(y)[i] = v;
+    store4(out, i, v);
   }
 }
 
@@ -69,8 +78,8 @@ __device__ __forceinline__ float wave_sum(float v) {
 // One wave per row of N4 * 256 columns: lane l holds float4 columns l + 64 j.
 // The mean and the (biased) variance are two exact passes over the row held
 // in registers, as torch.nn.LayerNorm defines them.
-template <int N4>
-__global__ __launch_bounds__(ET) void bias_residual_ln_kernel(float* out, float* ln_out, const float* x, const float* y,
+template <int N4, typename TN>
+__global__ __launch_bounds__(ET) void bias_residual_ln_kernel(float* out, TN* ln_out, const float* x, const float* y,
                                                               const float* bias, const float* gamma, const float* beta,
                                                               int64_t rows, int64_t seq_len, const int32_t* valid_len,
                                                               int mode, float eps, int zero_ln_padded) {
@@ -115,7 +124,7 @@ __global__ __launch_bounds__(ET) void bias_residual_ln_kernel(float* out, float*
     float4_t n;
 #pragma unroll
     for (int e = 0; e < 4; ++e) n[e] = zero ? 0.f : (r[j][e] - mean) * rstd * gv[e] + hv[e];
-    reinterpret_cast<float4_t*>(ln_out)[row * C4 + c] = n;
+    store4(ln_out, row * C4 + c, n);
   }
 }
 
@@ -142,22 +151,51 @@ extern "C" int tj_bias_residual(float* out, const float* x, const float* y, cons
   return tjh::launch_status();
 }
 
-extern "C" int tj_bias_gelu(float* y, const float* bias, int64_t rows, int64_t cols, hipStream_t stream) {
+extern "C" int tj_bias_gelu(float* y, const float* bias, int64_t rows, int64_t cols, void* out_f16,
+                            hipStream_t stream) {
   if (rows < 0 || cols <= 0) return TJ_ERR_SHAPE;
   if (cols % 4 != 0) return TJ_ERR_UNSUPPORTED;
   if (rows == 0) return TJ_OK;
   if (!y || !bias) return TJ_ERR_SHAPE;
-  if (!tjh::aligned16(y) || !tjh::aligned16(bias)) return TJ_ERR_ALIGN;
+  if (!tjh::aligned16(y) || !tjh::aligned16(bias) || (reinterpret_cast<uintptr_t>(out_f16) & 7u)) return TJ_ERR_ALIGN;
   const int64_t n4 = rows * (cols / 4);
-  hipLaunchKernelGGL(tj::bias_gelu_kernel, dim3(tj::grid_for(n4)), dim3(tj::ET), 0, stream, y, bias, n4, cols / 4);
+  if (out_f16 != nullptr) {
+    const int64_t ob = reinterpret_cast<int64_t>(out_f16), yb = reinterpret_cast<int64_t>(y);
+    if (ob < yb + rows * cols * 4 && yb < ob + rows * cols * 2) return TJ_ERR_SHAPE;  // no overlap with y
+    hipLaunchKernelGGL(tj::bias_gelu_kernel<half_t>, dim3(tj::grid_for(n4)), dim3(tj::ET), 0, stream, y,
+                       static_cast<half_t*>(out_f16), bias, n4, cols / 4);
+  } else {
+    hipLaunchKernelGGL(tj::bias_gelu_kernel<float>, dim3(tj::grid_for(n4)), dim3(tj::ET), 0, stream, y, y, bias, n4,
+                       cols / 4);
+  }
   return tjh::launch_status();
 }
 
-extern "C" int tj_bias_residual_layernorm(float* out, float* ln_out, const float* x, const float* y,
+namespace {
+
+template <typename TN>
+int launch_brl(float* out, TN* ln_out, const float* x, const float* y, const float* bias, const float* gamma,
+               const float* beta, int64_t rows, int64_t cols, int64_t seq_len, const int32_t* vl, int mode, float eps,
+               int zero_ln_padded, hipStream_t stream) {
+  const dim3 grid((unsigned)((rows + tj::ET / 64 - 1) / (tj::ET / 64)));
+  switch (cols / 256) {
+    case 1: hipLaunchKernelGGL((tj::bias_residual_ln_kernel<1, TN>), grid, dim3(tj::ET), 0, stream, out, ln_out, x, y, bias, gamma, beta, rows, seq_len, vl, mode, eps, zero_ln_padded); break;
+    case 2: hipLaunchKernelGGL((tj::bias_residual_ln_kernel<2, TN>), grid, dim3(tj::ET), 0, stream, out, ln_out, x, y, bias, gamma, beta, rows, seq_len, vl, mode, eps, zero_ln_padded); break;
+    case 4: hipLaunchKernelGGL((tj::bias_residual_ln_kernel<4, TN>), grid, dim3(tj::ET), 0, stream, out, ln_out, x, y, bias, gamma, beta, rows, seq_len, vl, mode, eps, zero_ln_padded); break;
+    case 8: hipLaunchKernelGGL((tj::bias_residual_ln_kernel<8, TN>), grid, dim3(tj::ET), 0, stream, out, ln_out, x, y, bias, gamma, beta, rows, seq_len, vl, mode, eps, zero_ln_padded); break;
+    default: return TJ_ERR_UNSUPPORTED;
+  }
+  return tjh::launch_status();
+}
+
+}  // namespace
+
+extern "C" int tj_bias_residual_layernorm(float* out, void* ln_out, int ln_dtype, const float* x, const float* y,
                                           const float* bias, const float* gamma, const float* beta, int64_t rows,
                                           int64_t cols, int64_t seq_len, const int32_t* valid_len, int mode,
                                           float eps, int zero_ln_padded, hipStream_t stream) {
   if (rows < 0 || cols <= 0 || seq_len <= 0 || mode < 0 || mode > 2 || !(eps >= 0.f)) return TJ_ERR_SHAPE;
+  if (ln_dtype != TJ_F32 && ln_dtype != TJ_F16) return TJ_ERR_DTYPE;
   if ((mode != 0 || zero_ln_padded) && valid_len != nullptr && rows % seq_len != 0) return TJ_ERR_SHAPE;
   if (cols % 256 != 0 || cols > 2048) return TJ_ERR_UNSUPPORTED;
   if (rows == 0) return TJ_OK;
@@ -165,16 +203,13 @@ extern "C" int tj_bias_residual_layernorm(float* out, float* ln_out, const float
   for (const void* p : {(const void*)out, (const void*)ln_out, (const void*)x, (const void*)y, (const void*)bias,
                         (const void*)gamma, (const void*)beta})
     if (!tjh::aligned16(p)) return TJ_ERR_ALIGN;
-  if ((int64_t)ln_out < (int64_t)out + rows * cols * 4 && (int64_t)out < (int64_t)ln_out + rows * cols * 4)
+  const int64_t ln_bytes = rows * cols * tjh::elem_size(ln_dtype);
+  if ((int64_t)ln_out < (int64_t)out + rows * cols * 4 && (int64_t)out < (int64_t)ln_out + ln_bytes)
     return TJ_ERR_SHAPE;  // the norm output must not overlap the residual stream
-  const dim3 grid((unsigned)((rows + tj::ET / 64 - 1) / (tj::ET / 64)));
   const int32_t* vl = (mode == 0 && !zero_ln_padded) ? nullptr : valid_len;
-  switch (cols / 256) {
-    case 1: hipLaunchKernelGGL(tj::bias_residual_ln_kernel<1>, grid, dim3(tj::ET), 0, stream, out, ln_out, x, y, bias, gamma, beta, rows, seq_len, vl, mode, eps, zero_ln_padded); break;
-    case 2: hipLaunchKernelGGL(tj::bias_residual_ln_kernel<2>, grid, dim3(tj::ET), 0, stream, out, ln_out, x, y, bias, gamma, beta, rows, seq_len, vl, mode, eps, zero_ln_padded); break;
-    case 4: hipLaunchKernelGGL(tj::bias_residual_ln_kernel<4>, grid, dim3(tj::ET), 0, stream, out, ln_out, x, y, bias, gamma, beta, rows, seq_len, vl, mode, eps, zero_ln_padded); break;
-    case 8: hipLaunchKernelGGL(tj::bias_residual_ln_kernel<8>, grid, dim3(tj::ET), 0, stream, out, ln_out, x, y, bias, gamma, beta, rows, seq_len, vl, mode, eps, zero_ln_padded); break;
-    default: return TJ_ERR_UNSUPPORTED;
-  }
-  return tjh::launch_status();
+  if (ln_dtype == TJ_F16)
+    return launch_brl(out, static_cast<half_t*>(ln_out), x, y, bias, gamma, beta, rows, cols, seq_len, vl, mode, eps,
+                      zero_ln_padded, stream);
+  return launch_brl(out, static_cast<float*>(ln_out), x, y, bias, gamma, beta, rows, cols, seq_len, vl, mode, eps,
+                    zero_ln_padded, stream);
 }

@@ -27,6 +27,10 @@ TJ_ERR_SCRATCH = 7
 TJ_F32 = 0
 TJ_F16 = 1
 
+#: The C ABI these bindings describe (tj_abi_version); a library built from
+#: other sources is refused at load time.
+ABI_VERSION = 2
+
 _i64 = ctypes.c_int64
 _i64p = ctypes.POINTER(ctypes.c_int64)
 _vp = ctypes.c_void_p
@@ -65,10 +69,10 @@ SIGNATURES = {
          _f32, _i64, _i64, _vp, _vp, _vp, ctypes.c_size_t, _vp],
     ),
     "tj_bias_residual": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _int, _vp]),
-    "tj_bias_gelu": (_int, [_vp, _vp, _i64, _i64, _vp]),
+    "tj_bias_gelu": (_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
     "tj_bias_residual_layernorm": (
         _int,
-        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _int, _f32, _int, _vp],
+        [_vp, _vp, _int, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _int, _f32, _int, _vp],
     ),
     "tj_quad_apply": (
         _int,
@@ -112,6 +116,11 @@ def lib() -> ctypes.CDLL:
                     raise LibraryMissingError(f"{LIB_PATH} does not export {name}") from err
                 fn.restype = res
                 fn.argtypes = args
+            version = handle.tj_abi_version()
+            if version != ABI_VERSION:
+                raise LibraryMissingError(
+                    f"{LIB_PATH} has C ABI version {version}, these bindings expect {ABI_VERSION}: "
+                    "rebuild it with `python -m techjam_amd.build`")
             _lib = handle
     return _lib
 

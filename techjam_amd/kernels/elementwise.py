@@ -57,23 +57,28 @@ def bias_residual(x: torch.Tensor, y: torch.Tensor, bias: torch.Tensor, valid_le
     return out
 
 
-def bias_gelu(y: torch.Tensor, bias: torch.Tensor) -> Optional[torch.Tensor]:
-    """``gelu(y + bias)`` (exact form) in place; ``y`` ``[..., C]``."""
+def bias_gelu(y: torch.Tensor, bias: torch.Tensor, out_f16: bool = False) -> Optional[torch.Tensor]:
+    """``gelu(y + bias)`` (exact form); ``y`` ``[..., C]``. In place, or with
+    ``out_f16`` into a new fp16 tensor (``y`` unchanged) -- the operand of an
+    fp16 GEMM."""
     if bias.ndim != 1 or y.shape[-1] != bias.shape[0] or not _ok(y, bias):
         return None
+    out = torch.empty(y.shape, dtype=torch.float16, device=y.device) if out_f16 else None
     code = _lib.lib().tj_bias_gelu(y.data_ptr(), bias.data_ptr(), y.numel() // y.shape[-1], y.shape[-1],
-                                   _stream_ptr(y.device))
+                                   None if out is None else out.data_ptr(), _stream_ptr(y.device))
     _lib.check(code, "tj_bias_gelu")
-    return y
+    return y if out is None else out
 
 
 def bias_residual_layernorm(x: torch.Tensor, y: torch.Tensor, bias: torch.Tensor,
                             valid_len: Optional[torch.Tensor], mode: int, norm: torch.nn.LayerNorm,
-                            out: Optional[torch.Tensor] = None, zero_padded_norm: bool = False):
+                            out: Optional[torch.Tensor] = None, zero_padded_norm: bool = False,
+                            norm_dtype: torch.dtype = torch.float32):
     """``bias_residual`` and ``norm`` of its result in one pass: ``(out, norm(out))``.
 
     With ``zero_padded_norm`` the norm output of padded rows is zero (the final
-    ``masked_fill``). ``None`` when the shapes or the norm are not covered.
+    ``masked_fill``); ``norm_dtype`` float16 stores the norm as the operand of
+    an fp16 GEMM. ``None`` when the shapes or the norm are not covered.
     """
     c = x.shape[-1] if x.ndim == 3 else 0
     if (x.ndim != 3 or y.shape != x.shape or bias.shape != (c,) or c % 256 or c > 2048 or (c // 256) & (c // 256 - 1)
@@ -83,15 +88,17 @@ def bias_residual_layernorm(x: torch.Tensor, y: torch.Tensor, bias: torch.Tensor
     if valid_len is not None and (valid_len.dtype != torch.int32 or valid_len.shape != (x.shape[0],)
                                   or valid_len.device != x.device):
         return None
+    if norm_dtype not in (torch.float32, torch.float16):
+        raise ValueError(f"norm_dtype must be float32 or float16, not {norm_dtype}")
     _check_out(out, x)
     out = torch.empty_like(x) if out is None else out
-    ln = torch.empty_like(x)
-    if not _ok(x, y, bias, out, ln, norm.weight, norm.bias):
+    if not _ok(x, y, bias, out, norm.weight, norm.bias):
         return None
+    ln = torch.empty(x.shape, dtype=norm_dtype, device=x.device)
     b, s, _ = x.shape
     code = _lib.lib().tj_bias_residual_layernorm(
-        out.data_ptr(), ln.data_ptr(), x.data_ptr(), y.data_ptr(), bias.data_ptr(), norm.weight.data_ptr(),
-        norm.bias.data_ptr(), b * s, c, s, None if valid_len is None else valid_len.data_ptr(), mode,
+        out.data_ptr(), ln.data_ptr(), _lib.TJ_F16 if norm_dtype == torch.float16 else _lib.TJ_F32, x.data_ptr(),
+        y.data_ptr(), bias.data_ptr(), norm.weight.data_ptr(), norm.bias.data_ptr(), b * s, c, s, None if valid_len is None else valid_len.data_ptr(), mode,
         float(norm.eps), int(bool(zero_padded_norm)), _stream_ptr(x.device))
     _lib.check(code, "tj_bias_residual_layernorm")
     return out, ln

@@ -243,31 +243,34 @@ class EncoderBlock(nn.Module):
         attention output, the GELU output, weights) to fp16 -- the 10-bit
         mantissa of TF32 -- and accumulates in fp32; q, k, v leave their GEMM
         as fp16 (the attention kernel rounds them to fp16 anyway), the other
-        GEMM results stay fp32, and so do the residual stream, LayerNorms,
-        softmax and GELU."""
+        GEMM results stay fp32, and so do the residual stream, LayerNorm
+        statistics, softmax and GELU. The LayerNorm and GELU kernels write
+        their outputs directly as the fp16 operands (no separate cast pass);
+        only the final norm, the model's output, stays fp32."""
         from .kernels.elementwise import MODE_ZERO_OUT, MODE_ZERO_Y, bias_gelu, bias_residual_layernorm
 
         attn = self.attention
-        f32 = torch.float32
+        f32, f16 = torch.float32, torch.float16
         x, a = state
         state.clear()
-        if fp16_operands:
+        if fp16_operands and a.dtype != f16:  # the first block's norm1 is a torch LayerNorm
             a = a.half()
         ctx = attn.context(a, valid_token_mask, causal, valid_len)
         del a
         y = project(ctx, attn.out_proj.weight, attn.out_proj, "weight", f32)
         del ctx
-        x, a = _must(bias_residual_layernorm(x, y, attn.out_proj.bias, valid_len, MODE_ZERO_Y, self.norm2, out=y))
+        x, a = _must(bias_residual_layernorm(x, y, attn.out_proj.bias, valid_len, MODE_ZERO_Y, self.norm2, out=y,
+                                             norm_dtype=f16 if fp16_operands else f32))
         del y
-        if fp16_operands:
-            a = a.half()
         h = project(a, self.ffn_in.weight, self.ffn_in, "weight", f32)
         del a
-        _must(bias_gelu(h, self.ffn_in.bias))
-        y = project(h.half() if fp16_operands else h, self.ffn_out.weight, self.ffn_out, "weight", f32)
+        # GELU in place, or straight into the fp16 operand of the next GEMM
+        h = _must(bias_gelu(h, self.ffn_in.bias, out_f16=fp16_operands))
+        y = project(h, self.ffn_out.weight, self.ffn_out, "weight", f32)
         del h
         return _must(bias_residual_layernorm(x, y, self.ffn_out.bias, valid_len, MODE_ZERO_OUT, next_norm, out=y,
-                                             zero_padded_norm=last and valid_token_mask is not None))
+                                             zero_padded_norm=last and valid_token_mask is not None,
+                                             norm_dtype=f16 if fp16_operands and not last else f32))
 
 
 def _must(t):

@@ -50,7 +50,7 @@ def test_error_strings_are_distinct_and_never_null():
 def test_abi_version():
     from techjam_amd.kernels import _lib
 
-    assert _lib.lib().tj_abi_version() == 1
+    assert _lib.lib().tj_abi_version() == _lib.ABI_VERSION == 2
 
 
 def _strides(*s):
@@ -206,9 +206,11 @@ def test_block_tails_reject_bad_arguments_before_launching():
     assert L.tj_bias_residual(16, 16, 16, 16, 5, 8, 2, 16, 1, None) == _lib.TJ_ERR_SHAPE
     assert L.tj_bias_residual(16, 24, 16, 16, 4, 8, 2, None, 0, None) == _lib.TJ_ERR_ALIGN
     assert L.tj_bias_residual(16, 16, 16, 16, 0, 8, 2, None, 0, None) == _lib.TJ_OK
-    assert L.tj_bias_gelu(16, 16, 4, 6, None) == _lib.TJ_ERR_UNSUPPORTED
-    assert L.tj_bias_gelu(8, 16, 4, 8, None) == _lib.TJ_ERR_ALIGN
-    assert L.tj_bias_gelu(16, 16, -1, 8, None) == _lib.TJ_ERR_SHAPE
+    assert L.tj_bias_gelu(16, 16, 4, 6, None, None) == _lib.TJ_ERR_UNSUPPORTED
+    assert L.tj_bias_gelu(8, 16, 4, 8, None, None) == _lib.TJ_ERR_ALIGN
+    assert L.tj_bias_gelu(16, 16, -1, 8, None, None) == _lib.TJ_ERR_SHAPE
+    assert L.tj_bias_gelu(16, 16, 4, 8, 20, None) == _lib.TJ_ERR_ALIGN       # fp16 output 8-byte aligned
+    assert L.tj_bias_gelu(16, 16, 4, 8, 64, None) == _lib.TJ_ERR_SHAPE       # overlaps y
 
 
 def test_noalloc_guard_rejects_requests_beyond_its_scratch_before_launching():

@@ -111,3 +111,30 @@ def test_bias_residual_layernorm_in_place_and_unsupported_widths(cuda):
     for c in (64, 768, 4096):  # not a power-of-two multiple of 256 up to 2048
         x, y, bias, lens, _ = _case(cuda, c=c, seed=22)
         assert bias_residual_layernorm(x, y, bias, lens, MODE_ZERO_OUT, torch.nn.LayerNorm(c).to(cuda)) is None
+
+
+def test_fp16_outputs_are_the_fp32_results_rounded(cuda):
+    """With fp16 GEMM operands the GELU and LayerNorm kernels write the fp16
+    operand directly: the fp32 result rounded to fp16 (the cast pass it
+    replaces) -- bitwise for GELU; for the norm within one fp16 ulp (the
+    affine step may contract into an fma differently in the two instances)
+    -- with the fp32 residual stream unchanged."""
+    from techjam_amd.kernels.elementwise import MODE_ZERO_Y, bias_gelu, bias_residual_layernorm
+
+    x, y, bias, lens, _ = _case(cuda, c=1024, seed=31)
+    h = (y * 3).contiguous()
+    want = bias_gelu(h.clone(), bias)
+    got = bias_gelu(h, bias, out_f16=True)
+    assert got.dtype == torch.float16 and torch.equal(got, want.half())
+    assert torch.equal(h, (y * 3))  # the fp32 input is left as it was
+    norm = torch.nn.LayerNorm(1024).to(cuda)
+    with torch.no_grad():
+        norm.weight.normal_(1.0, 0.2)
+        norm.bias.normal_(0.0, 0.2)
+    out32, ln32 = bias_residual_layernorm(x, y, bias, lens, MODE_ZERO_Y, norm)
+    out16, ln16 = bias_residual_layernorm(x, y, bias, lens, MODE_ZERO_Y, norm, norm_dtype=torch.float16)
+    assert ln16.dtype == torch.float16 and torch.equal(out16, out32)
+    ulp = torch.where(ln32.abs() < 2 ** -14, torch.full_like(ln32, 2 ** -24),
+                      torch.exp2(torch.floor(torch.log2(ln32.abs())) - 10))
+    assert bool(((ln16.float() - ln32).abs() <= ulp).all())
+    assert (ln16 != ln32.half()).float().mean().item() < 1e-3

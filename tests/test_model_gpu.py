@@ -187,4 +187,4 @@ def test_hip_library_is_the_one_loaded(cuda):
     assert str(_lib.LIB_PATH).endswith("techjam_amd/lib/libtechjam_attn.so")
     with open("/proc/self/maps") as f:
         assert any("libtechjam_attn.so" in line for line in f)
-    assert handle.tj_abi_version() == 1
+    assert handle.tj_abi_version() == _lib.ABI_VERSION
