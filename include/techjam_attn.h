@@ -288,6 +288,15 @@ int tj_bias_residual(float* out, const float* x, const float* y, const float* bi
 int tj_bias_gelu(float* y, const float* bias, int64_t rows, int64_t cols, void* out_f16, hipStream_t stream);
 
 /*
+ * max(y + bias, 0), with tj_bias_gelu's two output forms. No counterpart in
+ * the reference model (pre-norm, exact GELU); it serves the optional
+ * post-norm / ReLU block, torch.nn.TransformerEncoderLayer(norm_first=False,
+ * activation="relu") semantics, in which the benchmark configuration of a
+ * one-layer post-norm encoder with a ReLU FFN is stated.
+ */
+int tj_bias_relu(float* y, const float* bias, int64_t rows, int64_t cols, void* out_f16, hipStream_t stream);
+
+/*
  * tj_bias_residual (same modes, out may alias x or y) fused with the
  * LayerNorm that reads its result next (torch_transformer_benchmark.py:140-145:
  * norm2 after the attention residual, the next block's norm1 or the final norm
@@ -297,8 +306,10 @@ int tj_bias_gelu(float* y, const float* bias, int64_t rows, int64_t cols, void* 
  * stored as ln_dtype (TJ_F32, or TJ_F16 when the norm feeds a GEMM with fp16
  * operands; the statistics are fp32 either way).
  * With zero_ln_padded, rows at or past valid_len get ln_out = 0 (the final
- * masked_fill). ln_out must not overlap out. cols must be 256, 512, 1024 or
- * 2048 (TJ_ERR_UNSUPPORTED otherwise); all pointers 16-byte aligned.
+ * masked_fill). out may be NULL: the sum is then not stored, only its norm
+ * (a post-norm block, whose residual stream is the norm of the sum). ln_out
+ * must overlap none of out, x, y. cols must be 256, 512, 1024 or 2048
+ * (TJ_ERR_UNSUPPORTED otherwise); all pointers 16-byte aligned.
  */
 int tj_bias_residual_layernorm(float* out, void* ln_out, int ln_dtype, const float* x, const float* y,
                                const float* bias, const float* gamma, const float* beta,

@@ -1,7 +1,7 @@
 // Version and error-string entry points of the C ABI.
 #include "tj_common.h"
 
-extern "C" int tj_abi_version(void) { return 2; }
+extern "C" int tj_abi_version(void) { return 3; }
 
 extern "C" const char* tj_error_string(int code) {
   switch (code) {

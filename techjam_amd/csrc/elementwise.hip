@@ -9,10 +9,14 @@
 //   tj_bias_gelu     : y = gelu(y + b), exact (erf) form, in place -- or
 //                      written as fp16 to a separate buffer, the operand of
 //                      the next GEMM when GEMMs take fp16 operands
+//   tj_bias_relu     : y = max(y + b, 0), the same two output forms (the
+//                      post-norm / ReLU block variant)
 //   tj_bias_residual_layernorm : one of the residual forms above, and in the
 //                      same pass n = LayerNorm(out) (the next block's norm, or
 //                      the final one), so that the norm does not read the
-//                      residual stream again; n in fp32 or fp16
+//                      residual stream again; n in fp32 or fp16. out may be
+//                      null when only n is wanted: in a post-norm block the
+//                      norm of the sum is the new residual stream
 //
 // Tensors are fp32 [rows, cols] row-major with cols % 4 == 0 and 16-byte
 // aligned bases; row r = b * seq_len + s is valid iff s < valid_len[b].
@@ -54,17 +58,22 @@ __global__ __launch_bounds__(ET) void bias_residual_kernel(float* out, const flo
   }
 }
 
-template <typename TO>
-__global__ __launch_bounds__(ET) void bias_gelu_kernel(float* y, TO* out, const float* bias, int64_t n4, int64_t c4) {
+enum Act { ACT_GELU, ACT_RELU };
+
+template <Act A>
+__device__ __forceinline__ float activate(float t) {
+  if constexpr (A == ACT_GELU) return 0.5f * t * (1.f + erff(t * 0.70710678118654752f));
+  else return t > 0.f ? t : 0.f;
+}
+
+template <Act A, typename TO>
+__global__ __launch_bounds__(ET) void bias_act_kernel(float* y, TO* out, const float* bias, int64_t n4, int64_t c4) {
   for (int64_t i = blockIdx.x * (int64_t)ET + threadIdx.x; i < n4; i += (int64_t)gridDim.x * ET) {
     const int64_t c = i % c4;
     float4_t v = reinterpret_cast<const float4_t*>(y)[i];
     const float4_t bv = reinterpret_cast<const float4_t*>(bias)[c];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float t = v[e] + bv[e];
-      v[e] = 0.5f * t * (1.f + erff(t * 0.70710678118654752f));
-    }
+    for (int e = 0; e < 4; ++e) v[e] = activate<A>(v[e] + bv[e]);
     store4(out, i, v);
   }
 }
@@ -103,7 +112,7 @@ __global__ __launch_bounds__(ET) void bias_residual_ln_kernel(float* out, TN* ln
       r[j][e] = mode == 2 ? (ok ? xv[e] + t : 0.f) : xv[e] + (ok ? t : 0.f);
       sum += r[j][e];
     }
-    reinterpret_cast<float4_t*>(out)[row * C4 + c] = r[j];
+    if (out != nullptr) reinterpret_cast<float4_t*>(out)[row * C4 + c] = r[j];
   }
   const float mean = wave_sum(sum) / (float)(C4 * 4);
   float sq = 0.f;
@@ -151,8 +160,10 @@ extern "C" int tj_bias_residual(float* out, const float* x, const float* y, cons
   return tjh::launch_status();
 }
 
-extern "C" int tj_bias_gelu(float* y, const float* bias, int64_t rows, int64_t cols, void* out_f16,
-                            hipStream_t stream) {
+namespace {
+
+template <tj::Act A>
+int bias_act(float* y, const float* bias, int64_t rows, int64_t cols, void* out_f16, hipStream_t stream) {
   if (rows < 0 || cols <= 0) return TJ_ERR_SHAPE;
   if (cols % 4 != 0) return TJ_ERR_UNSUPPORTED;
   if (rows == 0) return TJ_OK;
@@ -162,13 +173,25 @@ extern "C" int tj_bias_gelu(float* y, const float* bias, int64_t rows, int64_t c
   if (out_f16 != nullptr) {
     const int64_t ob = reinterpret_cast<int64_t>(out_f16), yb = reinterpret_cast<int64_t>(y);
     if (ob < yb + rows * cols * 4 && yb < ob + rows * cols * 2) return TJ_ERR_SHAPE;  // no overlap with y
-    hipLaunchKernelGGL(tj::bias_gelu_kernel<half_t>, dim3(tj::grid_for(n4)), dim3(tj::ET), 0, stream, y,
+    hipLaunchKernelGGL((tj::bias_act_kernel<A, half_t>), dim3(tj::grid_for(n4)), dim3(tj::ET), 0, stream, y,
                        static_cast<half_t*>(out_f16), bias, n4, cols / 4);
   } else {
-    hipLaunchKernelGGL(tj::bias_gelu_kernel<float>, dim3(tj::grid_for(n4)), dim3(tj::ET), 0, stream, y, y, bias, n4,
-                       cols / 4);
+    hipLaunchKernelGGL((tj::bias_act_kernel<A, float>), dim3(tj::grid_for(n4)), dim3(tj::ET), 0, stream, y, y, bias,
+                       n4, cols / 4);
   }
   return tjh::launch_status();
+}
+
+}  // namespace
+
+extern "C" int tj_bias_gelu(float* y, const float* bias, int64_t rows, int64_t cols, void* out_f16,
+                            hipStream_t stream) {
+  return bias_act<tj::ACT_GELU>(y, bias, rows, cols, out_f16, stream);
+}
+
+extern "C" int tj_bias_relu(float* y, const float* bias, int64_t rows, int64_t cols, void* out_f16,
+                            hipStream_t stream) {
+  return bias_act<tj::ACT_RELU>(y, bias, rows, cols, out_f16, stream);
 }
 
 namespace {
@@ -199,13 +222,17 @@ extern "C" int tj_bias_residual_layernorm(float* out, void* ln_out, int ln_dtype
   if ((mode != 0 || zero_ln_padded) && valid_len != nullptr && rows % seq_len != 0) return TJ_ERR_SHAPE;
   if (cols % 256 != 0 || cols > 2048) return TJ_ERR_UNSUPPORTED;
   if (rows == 0) return TJ_OK;
-  if (!out || !ln_out || !x || !y || !bias || !gamma || !beta) return TJ_ERR_SHAPE;
+  if (!ln_out || !x || !y || !bias || !gamma || !beta) return TJ_ERR_SHAPE;  // out may be null
   for (const void* p : {(const void*)out, (const void*)ln_out, (const void*)x, (const void*)y, (const void*)bias,
                         (const void*)gamma, (const void*)beta})
     if (!tjh::aligned16(p)) return TJ_ERR_ALIGN;
   const int64_t ln_bytes = rows * cols * tjh::elem_size(ln_dtype);
-  if ((int64_t)ln_out < (int64_t)out + rows * cols * 4 && (int64_t)out < (int64_t)ln_out + ln_bytes)
-    return TJ_ERR_SHAPE;  // the norm output must not overlap the residual stream
+  // The norm output may overlap neither the inputs nor the residual output:
+  // rows of an fp16 norm and of the fp32 operands differ in size, so a row's
+  // store could land on a row another wave has not read yet.
+  for (const void* p : {(const void*)out, (const void*)x, (const void*)y})
+    if (p != nullptr && (int64_t)ln_out < (int64_t)p + rows * cols * 4 && (int64_t)p < (int64_t)ln_out + ln_bytes)
+      return TJ_ERR_SHAPE;
   const int32_t* vl = (mode == 0 && !zero_ln_padded) ? nullptr : valid_len;
   if (ln_dtype == TJ_F16)
     return launch_brl(out, static_cast<half_t*>(ln_out), x, y, bias, gamma, beta, rows, cols, seq_len, vl, mode, eps,

@@ -186,6 +186,10 @@ class DispatchingTransformer(TransformerEncoder):
 
     def __init__(self, config: TransformerConfig) -> None:
         super().__init__(config)
+        if not self.norm_first or self.activation != "gelu":
+            raise UnsupportedCaseError(
+                "the dispatcher serves the reference model (pre-norm, exact GELU); run other block "
+                "variants on TransformerEncoder directly")
         case_id = case_for(config)
         if config_key(config) == CASE_14_CONFIG:
             attention_type = PolyOrExactSelfAttention

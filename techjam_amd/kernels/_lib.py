@@ -29,7 +29,7 @@ TJ_F16 = 1
 
 #: The C ABI these bindings describe (tj_abi_version); a library built from
 #: other sources is refused at load time.
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _i64 = ctypes.c_int64
 _i64p = ctypes.POINTER(ctypes.c_int64)
@@ -70,6 +70,7 @@ SIGNATURES = {
     ),
     "tj_bias_residual": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _int, _vp]),
     "tj_bias_gelu": (_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
+    "tj_bias_relu": (_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
     "tj_bias_residual_layernorm": (
         _int,
         [_vp, _vp, _int, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _int, _f32, _int, _vp],

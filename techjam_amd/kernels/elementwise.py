@@ -4,7 +4,8 @@
 ``masked_fill`` and bias add / exact GELU pairs that follow the block's
 projection GEMMs (``torch_transformer_benchmark.py:116-121``, ``:140-145``)
 with one pass each; ``bias_residual_layernorm`` also produces the LayerNorm of
-the residual stream that the next step reads. They return ``None`` for
+the residual stream that the next step reads. ``bias_relu`` serves the
+optional post-norm / ReLU block. They return ``None`` for
 layouts the kernels do not take (non-fp32, a last dimension that is not a
 multiple of 4 -- of 256 up to 2048 for the norm --, unaligned or
 non-contiguous tensors), and the caller then uses the plain tensor ops.
@@ -57,28 +58,39 @@ def bias_residual(x: torch.Tensor, y: torch.Tensor, bias: torch.Tensor, valid_le
     return out
 
 
+def _bias_act(name: str, y: torch.Tensor, bias: torch.Tensor, out_f16: bool) -> Optional[torch.Tensor]:
+    if bias.ndim != 1 or y.shape[-1] != bias.shape[0] or not _ok(y, bias):
+        return None
+    out = torch.empty(y.shape, dtype=torch.float16, device=y.device) if out_f16 else None
+    code = getattr(_lib.lib(), name)(y.data_ptr(), bias.data_ptr(), y.numel() // y.shape[-1], y.shape[-1],
+                                     None if out is None else out.data_ptr(), _stream_ptr(y.device))
+    _lib.check(code, name)
+    return y if out is None else out
+
+
 def bias_gelu(y: torch.Tensor, bias: torch.Tensor, out_f16: bool = False) -> Optional[torch.Tensor]:
     """``gelu(y + bias)`` (exact form); ``y`` ``[..., C]``. In place, or with
     ``out_f16`` into a new fp16 tensor (``y`` unchanged) -- the operand of an
     fp16 GEMM."""
-    if bias.ndim != 1 or y.shape[-1] != bias.shape[0] or not _ok(y, bias):
-        return None
-    out = torch.empty(y.shape, dtype=torch.float16, device=y.device) if out_f16 else None
-    code = _lib.lib().tj_bias_gelu(y.data_ptr(), bias.data_ptr(), y.numel() // y.shape[-1], y.shape[-1],
-                                   None if out is None else out.data_ptr(), _stream_ptr(y.device))
-    _lib.check(code, "tj_bias_gelu")
-    return y if out is None else out
+    return _bias_act("tj_bias_gelu", y, bias, out_f16)
+
+
+def bias_relu(y: torch.Tensor, bias: torch.Tensor, out_f16: bool = False) -> Optional[torch.Tensor]:
+    """``relu(y + bias)``, in place or into a new fp16 tensor, as :func:`bias_gelu`."""
+    return _bias_act("tj_bias_relu", y, bias, out_f16)
 
 
 def bias_residual_layernorm(x: torch.Tensor, y: torch.Tensor, bias: torch.Tensor,
                             valid_len: Optional[torch.Tensor], mode: int, norm: torch.nn.LayerNorm,
                             out: Optional[torch.Tensor] = None, zero_padded_norm: bool = False,
-                            norm_dtype: torch.dtype = torch.float32):
+                            norm_dtype: torch.dtype = torch.float32, keep_sum: bool = True):
     """``bias_residual`` and ``norm`` of its result in one pass: ``(out, norm(out))``.
 
     With ``zero_padded_norm`` the norm output of padded rows is zero (the final
     ``masked_fill``); ``norm_dtype`` float16 stores the norm as the operand of
-    an fp16 GEMM. ``None`` when the shapes or the norm are not covered.
+    an fp16 GEMM. Without ``keep_sum`` the sum is not stored and ``(None,
+    norm)`` comes back (a post-norm block keeps only the norm). ``None`` when
+    the shapes or the norm are not covered.
     """
     c = x.shape[-1] if x.ndim == 3 else 0
     if (x.ndim != 3 or y.shape != x.shape or bias.shape != (c,) or c % 256 or c > 2048 or (c // 256) & (c // 256 - 1)
@@ -90,14 +102,17 @@ def bias_residual_layernorm(x: torch.Tensor, y: torch.Tensor, bias: torch.Tensor
         return None
     if norm_dtype not in (torch.float32, torch.float16):
         raise ValueError(f"norm_dtype must be float32 or float16, not {norm_dtype}")
+    if not keep_sum and out is not None:
+        raise ValueError("out is not written when keep_sum is False")
     _check_out(out, x)
-    out = torch.empty_like(x) if out is None else out
-    if not _ok(x, y, bias, out, norm.weight, norm.bias):
+    if keep_sum and out is None:
+        out = torch.empty_like(x)
+    if not _ok(x, y, bias, norm.weight, norm.bias, *([out] if keep_sum else [])):
         return None
     ln = torch.empty(x.shape, dtype=norm_dtype, device=x.device)
     b, s, _ = x.shape
     code = _lib.lib().tj_bias_residual_layernorm(
-        out.data_ptr(), ln.data_ptr(), _lib.TJ_F16 if norm_dtype == torch.float16 else _lib.TJ_F32, x.data_ptr(),
+        None if out is None else out.data_ptr(), ln.data_ptr(), _lib.TJ_F16 if norm_dtype == torch.float16 else _lib.TJ_F32, x.data_ptr(),
         y.data_ptr(), bias.data_ptr(), norm.weight.data_ptr(), norm.bias.data_ptr(), b * s, c, s, None if valid_len is None else valid_len.data_ptr(), mode,
         float(norm.eps), int(bool(zero_padded_norm)), _stream_ptr(x.device))
     _lib.check(code, "tj_bias_residual_layernorm")

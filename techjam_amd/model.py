@@ -12,7 +12,7 @@ kernel through the C ABI instead of materialising a score tensor.
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import Optional
+from typing import Optional, Tuple
 
 import torch
 import torch.nn as nn
@@ -21,9 +21,20 @@ import torch.nn.functional as F
 from .kernels.attention import scaled_dot_product_attention
 
 
+ACTIVATIONS = ("gelu", "relu")
+
+
 @dataclass(frozen=True)
 class TransformerConfig:
-    """Static model shape; field names follow ``torch_transformer_benchmark.py:29-56``."""
+    """Static model shape; field names follow ``torch_transformer_benchmark.py:29-56``.
+
+    ``norm_first`` and ``activation`` select the block: the reference model is
+    pre-norm with exact GELU (the defaults); ``norm_first=False,
+    activation="relu"`` is the post-norm / ReLU block of
+    ``torch.nn.TransformerEncoderLayer(norm_first=False, activation="relu")``,
+    the wording some benchmark configurations are stated in. Config objects
+    without these fields (the reference harness's own) mean the defaults.
+    """
 
     batch_size: int
     seq_len: int
@@ -32,6 +43,8 @@ class TransformerConfig:
     ffn_dim: int
     num_layers: int
     causal: bool
+    norm_first: bool = True
+    activation: str = "gelu"
 
     def validate(self) -> None:
         for name in ("batch_size", "seq_len", "d_model", "num_heads", "ffn_dim", "num_layers"):
@@ -41,6 +54,18 @@ class TransformerConfig:
             raise ValueError(
                 f"d_model ({self.d_model}) must be divisible by num_heads ({self.num_heads})"
             )
+        if self.activation not in ACTIVATIONS:
+            raise ValueError(f"activation must be one of {ACTIVATIONS}, not {self.activation!r}")
+
+
+def block_variant(config) -> Tuple[bool, str]:
+    """``(norm_first, activation)`` of a config; the reference's block when the
+    config does not say."""
+    norm_first = bool(getattr(config, "norm_first", True))
+    activation = getattr(config, "activation", "gelu")
+    if activation not in ACTIVATIONS:
+        raise ValueError(f"activation must be one of {ACTIVATIONS}, not {activation!r}")
+    return norm_first, activation
 
 
 def config_key(config) -> tuple:
@@ -182,21 +207,40 @@ class HipSelfAttention(nn.Module):
 
 
 class EncoderBlock(nn.Module):
-    """Pre-norm residual block with exact GELU (``torch_transformer_benchmark.py:125-145``)."""
+    """Pre-norm residual block with exact GELU (``torch_transformer_benchmark.py:125-145``).
 
-    def __init__(self, d_model: int, num_heads: int, ffn_dim: int) -> None:
+    With ``norm_first=False`` the block is post-norm, ``x = norm1(x +
+    attention(x))`` then ``x = norm2(x + ffn(x))``, and ``activation="relu"``
+    puts ReLU in the FFN: ``torch.nn.TransformerEncoderLayer``'s semantics for
+    those options (dropout off). Same modules and parameter names either way;
+    padded rows are zeroed at the end of the block as in the reference.
+    """
+
+    def __init__(self, d_model: int, num_heads: int, ffn_dim: int, norm_first: bool = True,
+                 activation: str = "gelu") -> None:
         super().__init__()
+        if activation not in ACTIVATIONS:
+            raise ValueError(f"activation must be one of {ACTIVATIONS}, not {activation!r}")
+        self.norm_first = norm_first
+        self.activation = activation
         self.norm1 = nn.LayerNorm(d_model)
         self.attention = HipSelfAttention(d_model, num_heads)
         self.norm2 = nn.LayerNorm(d_model)
         self.ffn_in = Linear(d_model, ffn_dim)
         self.ffn_out = Linear(ffn_dim, d_model)
 
+    def _act(self, h: torch.Tensor) -> torch.Tensor:
+        return F.gelu(h, approximate="none") if self.activation == "gelu" else F.relu(h)
+
     def forward(self, x, valid_token_mask, causal, valid_len=None):
         if self._can_fuse(x, valid_token_mask, valid_len):
             return self._forward_fused(x, valid_token_mask, causal, valid_len)
-        x = x + self.attention(self.norm1(x), valid_token_mask, causal, valid_len=valid_len)
-        x = x + self.ffn_out(F.gelu(self.ffn_in(self.norm2(x)), approximate="none"))
+        if self.norm_first:
+            x = x + self.attention(self.norm1(x), valid_token_mask, causal, valid_len=valid_len)
+            x = x + self.ffn_out(self._act(self.ffn_in(self.norm2(x))))
+        else:
+            x = self.norm1(x + self.attention(x, valid_token_mask, causal, valid_len=valid_len))
+            x = self.norm2(x + self.ffn_out(self._act(self.ffn_in(x))))
         if valid_token_mask is not None:
             x = x.masked_fill(~valid_token_mask[..., None], 0)
         return x
@@ -206,22 +250,55 @@ class EncoderBlock(nn.Module):
                 and x.data_ptr() % 16 == 0 and x.shape[-1] % 4 == 0 and self.ffn_in.out_features % 4 == 0
                 and (valid_token_mask is None or valid_len is not None)
                 and self.attention.out_proj.bias is not None and self.ffn_in.bias is not None
-                and self.ffn_out.bias is not None)
+                and self.ffn_out.bias is not None
+                and (self.norm_first or self._post_norms_fusable(x)))
+
+    def _post_norms_fusable(self, x) -> bool:
+        c = x.shape[-1]
+        return (c in (256, 512, 1024, 2048)
+                and all(type(n) is nn.LayerNorm and n.elementwise_affine and n.bias is not None
+                        and n.weight.dtype == torch.float32 for n in (self.norm1, self.norm2)))
 
     def _forward_fused(self, x, valid_token_mask, causal, valid_len):
         """Same computation as the unfused forward; the projection GEMMs run
-        bias-free and each bias add, residual add, GELU and row zeroing is
-        folded into one pass over the GEMM output."""
-        from .kernels.elementwise import MODE_ZERO_OUT, MODE_ZERO_Y, bias_gelu, bias_residual
+        bias-free and each bias add, residual add, activation and row zeroing
+        is folded into one pass over the GEMM output (for the post-norm block
+        together with the LayerNorm that follows it)."""
+        if not self.norm_first:
+            return self._forward_fused_post(x, valid_token_mask, causal, valid_len)
+        from .kernels.elementwise import MODE_ZERO_OUT, MODE_ZERO_Y, bias_gelu, bias_relu, bias_residual
 
+        act = bias_gelu if self.activation == "gelu" else bias_relu
         attn = self.attention
         ctx = attn.context(self.norm1(x), valid_token_mask, causal, valid_len)
         y = _linear_f32(ctx, attn.out_proj.weight)
         x = _must(bias_residual(x, y, attn.out_proj.bias, valid_len, MODE_ZERO_Y, out=y))
         h = _linear_f32(self.norm2(x), self.ffn_in.weight)
-        _must(bias_gelu(h, self.ffn_in.bias))
+        _must(act(h, self.ffn_in.bias))
         y = _linear_f32(h, self.ffn_out.weight)
         return _must(bias_residual(x, y, self.ffn_out.bias, valid_len, MODE_ZERO_OUT, out=y))
+
+    def _forward_fused_post(self, x, valid_token_mask, causal, valid_len):
+        """The post-norm block: each residual pass stores only the LayerNorm of
+        its sum, which is the next residual stream; the second one zeroes the
+        padded rows of its norm (the block's final ``masked_fill``)."""
+        from .kernels.elementwise import MODE_PLAIN, MODE_ZERO_Y, bias_gelu, bias_relu, bias_residual_layernorm
+
+        act = bias_gelu if self.activation == "gelu" else bias_relu
+        attn = self.attention
+        ctx = attn.context(x, valid_token_mask, causal, valid_len)
+        y = _linear_f32(ctx, attn.out_proj.weight)
+        del ctx
+        _, x = _must(bias_residual_layernorm(x, y, attn.out_proj.bias, valid_len, MODE_ZERO_Y, self.norm1,
+                                             keep_sum=False))
+        del y
+        h = _linear_f32(x, self.ffn_in.weight)
+        _must(act(h, self.ffn_in.bias))
+        y = _linear_f32(h, self.ffn_out.weight)
+        del h
+        _, x = _must(bias_residual_layernorm(x, y, self.ffn_out.bias, valid_len, MODE_PLAIN, self.norm2,
+                                             zero_padded_norm=valid_token_mask is not None, keep_sum=False))
+        return x
 
     def _forward_fused_norms(self, state, valid_token_mask, causal, valid_len, next_norm, last,
                              fp16_operands=False):
@@ -247,7 +324,7 @@ class EncoderBlock(nn.Module):
         statistics, softmax and GELU. The LayerNorm and GELU kernels write
         their outputs directly as the fp16 operands (no separate cast pass);
         only the final norm, the model's output, stays fp32."""
-        from .kernels.elementwise import MODE_ZERO_OUT, MODE_ZERO_Y, bias_gelu, bias_residual_layernorm
+        from .kernels.elementwise import MODE_ZERO_OUT, MODE_ZERO_Y, bias_gelu, bias_relu, bias_residual_layernorm
 
         attn = self.attention
         f32, f16 = torch.float32, torch.float16
@@ -264,8 +341,9 @@ class EncoderBlock(nn.Module):
         del y
         h = project(a, self.ffn_in.weight, self.ffn_in, "weight", f32)
         del a
-        # GELU in place, or straight into the fp16 operand of the next GEMM
-        h = _must(bias_gelu(h, self.ffn_in.bias, out_f16=fp16_operands))
+        # the activation in place, or straight into the fp16 operand of the next GEMM
+        act = bias_gelu if self.activation == "gelu" else bias_relu
+        h = _must(act(h, self.ffn_in.bias, out_f16=fp16_operands))
         y = project(h, self.ffn_out.weight, self.ffn_out, "weight", f32)
         del h
         return _must(bias_residual_layernorm(x, y, self.ffn_out.bias, valid_len, MODE_ZERO_OUT, next_norm, out=y,
@@ -290,11 +368,14 @@ class TransformerEncoder(nn.Module):
     def __init__(self, config: TransformerConfig) -> None:
         super().__init__()
         self.config = config
+        self.norm_first, self.activation = block_variant(config)
         self.layers = nn.ModuleList(
-            EncoderBlock(config.d_model, config.num_heads, config.ffn_dim)
+            EncoderBlock(config.d_model, config.num_heads, config.ffn_dim, self.norm_first, self.activation)
             for _ in range(config.num_layers)
         )
-        self.final_norm = nn.LayerNorm(config.d_model)
+        # A post-norm stack ends in its last block's norm (torch.nn.TransformerEncoder
+        # with norm=None); only the pre-norm stack has a final LayerNorm.
+        self.final_norm = nn.LayerNorm(config.d_model) if self.norm_first else nn.Identity()
 
     def forward_layers(self, x, valid_token_mask=None, valid_len=None):
         if self.gemm_operands not in ("fp32", "fp16"):
@@ -304,9 +385,11 @@ class TransformerEncoder(nn.Module):
         if self.gemm_operands == "fp16":
             from .errors import UnsupportedCaseError
 
-            raise UnsupportedCaseError("fp16 GEMM operands are implemented on the fused GPU path only")
+            raise UnsupportedCaseError("fp16 GEMM operands are implemented on the fused pre-norm GPU path only")
         for layer in self.layers:
             x = layer(x, valid_token_mask, self.config.causal, valid_len=valid_len)
+        if not self.norm_first:
+            return x  # each block already ended in its norm and its row zeroing
         x = self.final_norm(x)
         if valid_token_mask is not None:
             x.masked_fill_(~valid_token_mask[..., None], 0)  # x is the norm's fresh output
@@ -314,6 +397,8 @@ class TransformerEncoder(nn.Module):
 
     def _can_fuse_norms(self, x, valid_token_mask, valid_len) -> bool:
         d = x.shape[-1] if x.ndim == 3 else 0
+        if not self.norm_first:
+            return False
         norms = [m for layer in self.layers for m in (layer.norm1, layer.norm2)] + [self.final_norm]
         return (len(self.layers) > 0 and d in (256, 512, 1024, 2048)
                 and all(layer._can_fuse(x, valid_token_mask, valid_len) for layer in self.layers)

@@ -50,7 +50,7 @@ def test_error_strings_are_distinct_and_never_null():
 def test_abi_version():
     from techjam_amd.kernels import _lib
 
-    assert _lib.lib().tj_abi_version() == _lib.ABI_VERSION == 2
+    assert _lib.lib().tj_abi_version() == _lib.ABI_VERSION == 3
 
 
 def _strides(*s):
@@ -211,6 +211,22 @@ def test_block_tails_reject_bad_arguments_before_launching():
     assert L.tj_bias_gelu(16, 16, -1, 8, None, None) == _lib.TJ_ERR_SHAPE
     assert L.tj_bias_gelu(16, 16, 4, 8, 20, None) == _lib.TJ_ERR_ALIGN       # fp16 output 8-byte aligned
     assert L.tj_bias_gelu(16, 16, 4, 8, 64, None) == _lib.TJ_ERR_SHAPE       # overlaps y
+    assert L.tj_bias_relu(16, 16, 4, 6, None, None) == _lib.TJ_ERR_UNSUPPORTED
+    assert L.tj_bias_relu(8, 16, 4, 8, None, None) == _lib.TJ_ERR_ALIGN
+    assert L.tj_bias_relu(16, 16, 4, 8, 64, None) == _lib.TJ_ERR_SHAPE       # overlaps y
+    assert L.tj_bias_relu(16, 16, 0, 8, None, None) == _lib.TJ_OK
+    # tj_bias_residual_layernorm(out, ln_out, ln_dtype, x, y, bias, gamma, beta, rows, cols, seq_len,
+    # valid_len, mode, eps, zero_ln_padded, stream) on 4 x 256 fp32 rows (4 KiB): out may be null,
+    # the norm output may overlap nothing else
+    ln = L.tj_bias_residual_layernorm
+    x, y, g = 1 << 20, 1 << 21, 1 << 22
+    assert ln(None, None, _lib.TJ_F32, x, y, g, g, g, 4, 256, 4, None, 0, 1e-5, 0, None) == _lib.TJ_ERR_SHAPE
+    assert ln(None, x + 2048, _lib.TJ_F32, x, y, g, g, g, 4, 256, 4, None, 0, 1e-5, 0, None) == _lib.TJ_ERR_SHAPE
+    assert ln(None, y, _lib.TJ_F16, x, y, g, g, g, 4, 256, 4, None, 0, 1e-5, 0, None) == _lib.TJ_ERR_SHAPE
+    o = 1 << 23
+    assert ln(o, o + 2048, _lib.TJ_F32, x, y, g, g, g, 4, 256, 4, None, 0, 1e-5, 0, None) == _lib.TJ_ERR_SHAPE
+    assert ln(None, g, _lib.TJ_F32, x, y, g, g, g, 4, 384, 4, None, 0, 1e-5, 0, None) == _lib.TJ_ERR_UNSUPPORTED
+    assert ln(None, g + 8, _lib.TJ_F32, x, y, g, g, g, 4, 256, 4, None, 0, 1e-5, 0, None) == _lib.TJ_ERR_ALIGN
 
 
 def test_noalloc_guard_rejects_requests_beyond_its_scratch_before_launching():

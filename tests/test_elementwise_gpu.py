@@ -138,3 +138,37 @@ def test_fp16_outputs_are_the_fp32_results_rounded(cuda):
                       torch.exp2(torch.floor(torch.log2(ln32.abs())) - 10))
     assert bool(((ln16.float() - ln32).abs() <= ulp).all())
     assert (ln16 != ln32.half()).float().mean().item() < 1e-3
+
+
+def test_bias_relu_matches_relu(cuda):
+    from techjam_amd.kernels.elementwise import bias_relu
+
+    x, y, bias, _, _ = _case(cuda, c=256, seed=7)
+    want = F.relu(y + bias)
+    h16 = bias_relu(y.clone(), bias, out_f16=True)
+    assert h16.dtype == torch.float16 and torch.equal(h16, want.half())
+    got = bias_relu(y, bias)
+    assert got.data_ptr() == y.data_ptr() and torch.equal(got, want)
+
+
+@pytest.mark.parametrize("masked", [False, True])
+@torch.no_grad()
+def test_layernorm_only_pass_matches_the_full_pass(cuda, masked):
+    """Without ``keep_sum`` (the post-norm block) the norm is bitwise the one
+    the pass computes when it also stores the sum."""
+    from techjam_amd.kernels.elementwise import MODE_PLAIN, MODE_ZERO_Y, bias_residual_layernorm
+
+    x, y, bias, lens, mask = _case(cuda, c=512, seed=8)
+    norm = torch.nn.LayerNorm(512).to(cuda)
+    norm.weight.uniform_(0.5, 1.5)
+    norm.bias.uniform_(-0.5, 0.5)
+    vl = lens if masked else None
+    for mode in (MODE_PLAIN, MODE_ZERO_Y):
+        s_full, ln_full = bias_residual_layernorm(x, y, bias, vl, mode, norm, zero_padded_norm=masked)
+        s_none, ln_only = bias_residual_layernorm(x, y, bias, vl, mode, norm, zero_padded_norm=masked,
+                                                  keep_sum=False)
+        assert s_none is None and torch.equal(ln_only, ln_full)
+        want = F.layer_norm(s_full, (512,), norm.weight, norm.bias, norm.eps)
+        if masked:
+            want = want.masked_fill(~mask[..., None], 0)
+        assert float((ln_only - want).abs().max()) < 1e-5
