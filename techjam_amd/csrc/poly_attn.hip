@@ -199,29 +199,11 @@ struct TokTile {
   }
 };
 
-// Workgroup barrier without the memory fences of __syncthreads(): callers wait
-// for their own LDS traffic explicitly (s_waitcnt) before it. The empty asm
-// statements keep the compiler from moving memory accesses across.
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 __device__ __forceinline__ half8_t mul8(half8_t x, half_t s) {
   half8_t r;
 #pragma unroll
   for (int j = 0; j < 8; ++j) r[j] = x[j] * s;
   return r;
-}
-
-// f(integral_constant<int, I>) for I = B .. E-1, each with compile-time I.
-template <int B, int E, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (B < E) {
-    f(std::integral_constant<int, B>{});
-    static_for<B + 1, E>(f);
-  }
 }
 
 // ---------------------------------------------------------------------------

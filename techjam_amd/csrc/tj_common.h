@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "techjam_attn.h"
 
 typedef _Float16 half_t;
@@ -31,6 +33,29 @@ __device__ __forceinline__ float16_t mfma32(half8_t a, half8_t b, float16_t c) {
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Workgroup barrier without the memory fences of __syncthreads() (which also
+// wait for every global load in flight): callers wait for their own LDS
+// traffic explicitly (s_waitcnt) before it. The empty asm statements keep the
+// compiler from moving memory accesses across.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// s_waitcnt lgkmcnt(0) alone (vmcnt and expcnt at their maxima): this wave's
+// LDS accesses are done, its global loads may stay in flight.
+__device__ __forceinline__ void wait_lds() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// f(integral_constant<int, I>) for I = B .. E-1, each with compile-time I.
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
 
 // Reductions over the lane pair (l, l ^ 32) through v_permlane32_swap, a VALU
 // op on gfx950, instead of an LDS permute. With both operands equal the swap
