@@ -560,7 +560,7 @@ int attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype, in
   if (B < 0 || H <= 0 || S < 0 || D <= 0) return TJ_ERR_SHAPE;
   // Tile indices fit 31 bits; the launch also checks that its grid fits the
   // 32-bit dispatch size.
-  if (B * H * ((S + 127) / 128) >= (int64_t(1) << 31) || S >= (int64_t(1) << 30)) return TJ_ERR_SHAPE;
+  if (S >= (int64_t(1) << 30) || !tjh::product_below(int64_t(1) << 31, {B, H, (S + 127) / 128})) return TJ_ERR_SHAPE;
   if (D != 32 && D != 64 && D != 128 && D != 256) return TJ_ERR_UNSUPPORTED;
   if (B == 0 || S == 0) return TJ_OK;
   if (!q || !k || !v || !o) return TJ_ERR_SHAPE;
@@ -569,10 +569,8 @@ int attn_fwd(const void* q, const void* k, const void* v, void* o, int dtype, in
     return TJ_ERR_ALIGN;
   if ((reinterpret_cast<uintptr_t>(q_bias) | reinterpret_cast<uintptr_t>(v_bias)) & 15u) return TJ_ERR_ALIGN;
   // K and V rows of one (b, h) are addressed with 31-bit byte offsets.
-  for (const int64_t* st : {k_strides, v_strides}) {
-    if (st[2] < 0 || ((S - 1) * st[2] + D) * tjh::elem_size(dtype) >= (int64_t(1) << 31))
-      return TJ_ERR_UNSUPPORTED;
-  }
+  for (const int64_t* st : {k_strides, v_strides})
+    if (!tjh::span_below_2g(S, st[2], D, tjh::elem_size(dtype))) return TJ_ERR_UNSUPPORTED;
 
   tj::AttnArgs a;
   a.q = q; a.k = k; a.v = v; a.o = o;

@@ -137,6 +137,10 @@ __global__ __launch_bounds__(ET) void bias_residual_ln_kernel(float* out, TN* ln
   }
 }
 
+// Element counts above this are refused (far beyond any device memory), so
+// byte counts of the operands fit 64 bits.
+constexpr int64_t kMaxElements = int64_t(1) << 56;
+
 unsigned grid_for(int64_t n4) {
   const int64_t blocks = (n4 + ET - 1) / ET;
   return (unsigned)(blocks < 256 * 32 ? blocks : 256 * 32);
@@ -149,6 +153,7 @@ extern "C" int tj_bias_residual(float* out, const float* x, const float* y, cons
                                 int64_t cols, int64_t seq_len, const int32_t* valid_len, int mode,
                                 hipStream_t stream) {
   if (rows < 0 || cols <= 0 || seq_len <= 0 || mode < 0 || mode > 2) return TJ_ERR_SHAPE;
+  if (!tjh::product_below(tj::kMaxElements, {rows, cols})) return TJ_ERR_SHAPE;
   if (mode != 0 && valid_len != nullptr && rows % seq_len != 0) return TJ_ERR_SHAPE;
   if (cols % 4 != 0) return TJ_ERR_UNSUPPORTED;
   if (rows == 0) return TJ_OK;
@@ -164,7 +169,7 @@ namespace {
 
 template <tj::Act A>
 int bias_act(float* y, const float* bias, int64_t rows, int64_t cols, void* out_f16, hipStream_t stream) {
-  if (rows < 0 || cols <= 0) return TJ_ERR_SHAPE;
+  if (rows < 0 || cols <= 0 || !tjh::product_below(tj::kMaxElements, {rows, cols})) return TJ_ERR_SHAPE;
   if (cols % 4 != 0) return TJ_ERR_UNSUPPORTED;
   if (rows == 0) return TJ_OK;
   if (!y || !bias) return TJ_ERR_SHAPE;
@@ -218,6 +223,7 @@ extern "C" int tj_bias_residual_layernorm(float* out, void* ln_out, int ln_dtype
                                           int64_t cols, int64_t seq_len, const int32_t* valid_len, int mode,
                                           float eps, int zero_ln_padded, hipStream_t stream) {
   if (rows < 0 || cols <= 0 || seq_len <= 0 || mode < 0 || mode > 2 || !(eps >= 0.f)) return TJ_ERR_SHAPE;
+  if (!tjh::product_below(tj::kMaxElements, {rows, cols})) return TJ_ERR_SHAPE;
   if (ln_dtype != TJ_F32 && ln_dtype != TJ_F16) return TJ_ERR_DTYPE;
   if ((mode != 0 || zero_ln_padded) && valid_len != nullptr && rows % seq_len != 0) return TJ_ERR_SHAPE;
   if (cols % 256 != 0 || cols > 2048) return TJ_ERR_UNSUPPORTED;

@@ -868,6 +868,7 @@ extern "C" size_t tj_poly_workspace_bytes(int64_t B, int64_t H, int64_t S, int64
   (void)S;
   (void)chunk;
   if (B <= 0 || H <= 0 || D != tj::PD) return 0;
+  if (!tjh::product_below(std::numeric_limits<int64_t>::max() / int64_t(tj::kPerHead), {B, H})) return 0;
   return size_t(B * H) * tj::kPerHead;
 }
 
@@ -882,16 +883,16 @@ extern "C" int tj_poly_attn_fwd(const void* q, const void* k, const void* v, voi
   if (B < 0 || H <= 0 || S < 0 || D <= 0 || chunk <= 0 || exact_prefix < 0 || !(scale > 0.f)) return TJ_ERR_SHAPE;
   if (D != tj::PD || chunk != tj::PC) return TJ_ERR_UNSUPPORTED;
   if (B == 0 || S == 0 || exact_prefix >= S) return TJ_OK;
-  if ((B * H + tj::kNumXcd) * tj::NROLE >= (int64_t(1) << 31) || S >= (int64_t(1) << 30)) return TJ_ERR_SHAPE;
+  if (S >= (int64_t(1) << 30) ||
+      !tjh::product_below((int64_t(1) << 31) / tj::NROLE - tj::kNumXcd, {B, H}))
+    return TJ_ERR_SHAPE;
   if (!q || !k || !v || !o || !coeffs) return TJ_ERR_SHAPE;
   if (!tjh::view_ok(q, q_strides, dtype) || !tjh::view_ok(k, k_strides, dtype) ||
       !tjh::view_ok(v, v_strides, dtype) || !tjh::view_ok(o, o_strides, dtype))
     return TJ_ERR_ALIGN;
   // K and V rows of one (b, h) are addressed with 31-bit byte offsets.
-  for (const int64_t* st : {k_strides, v_strides}) {
-    if (st[2] < 0 || ((S - 1) * st[2] + D) * tjh::elem_size(dtype) >= (int64_t(1) << 31))
-      return TJ_ERR_UNSUPPORTED;
-  }
+  for (const int64_t* st : {k_strides, v_strides})
+    if (!tjh::span_below_2g(S, st[2], D, tjh::elem_size(dtype))) return TJ_ERR_UNSUPPORTED;
   const size_t need = size_t(B * H) * tj::kPerHead;
   if (workspace == nullptr || workspace_bytes < need || !tjh::aligned16(workspace)) return TJ_ERR_WORKSPACE;
 

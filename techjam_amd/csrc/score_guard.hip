@@ -198,7 +198,10 @@ __global__ __launch_bounds__(GT) void score_guard_final_kernel(GuardArgs a, cons
 
 extern "C" size_t tj_score_guard_workspace_bytes(int64_t B, int64_t H, int64_t n_samples) {
   if (B <= 0 || H <= 0 || n_samples <= 0 || n_samples >= (int64_t(1) << 30)) return 0;
-  return size_t(B) * size_t(H) * size_t(tj::guard_blocks((int)n_samples)) * 3 * sizeof(double);
+  const int64_t per_block = 3 * sizeof(double);
+  const int64_t blocks = tj::guard_blocks((int)n_samples);
+  if (!tjh::product_below(std::numeric_limits<int64_t>::max() / per_block, {B, H, blocks})) return 0;
+  return size_t(B) * size_t(H) * size_t(blocks) * per_block;
 }
 
 // Fixed scratch of tj_score_guard_noalloc: room for the partial sums of
@@ -256,9 +259,10 @@ int guard_check(const void* q, const void* k, int dtype, int64_t B, int64_t H, i
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k)) % (4 * elt) != 0) return TJ_ERR_ALIGN;
   for (int i = 0; i < 3; ++i)
     if (q_strides[i] % 4 != 0 || k_strides[i] % 4 != 0) return TJ_ERR_ALIGN;
-  if (B * H >= (int64_t(1) << 31) || S >= (int64_t(1) << 31)) return TJ_ERR_SHAPE;
+  if (!tjh::product_below(int64_t(1) << 31, {B, H}) || S >= (int64_t(1) << 31)) return TJ_ERR_SHAPE;
   const size_t need = tj_score_guard_workspace_bytes(B, H, n_samples);
-  if (need == 0 || B * H * tj::guard_blocks((int)n_samples) >= (int64_t(1) << 31)) return TJ_ERR_SHAPE;
+  if (need == 0 || !tjh::product_below(int64_t(1) << 31, {B, H, tj::guard_blocks((int)n_samples)}))
+    return TJ_ERR_SHAPE;
   return TJ_OK;
 }
 

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <initializer_list>
+#include <limits>
 #include <type_traits>
 
 #include "techjam_attn.h"
@@ -124,6 +126,22 @@ namespace tjh {
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 inline int elem_size(int dtype) { return dtype == TJ_F32 ? 4 : (dtype == TJ_F16 ? 2 : 0); }
+
+// The product of non-negative factors is below `limit`, decided without
+// overflowing (a negative factor or an overflowing product is not below).
+inline bool product_below(int64_t limit, std::initializer_list<int64_t> factors) {
+  int64_t p = 1;
+  for (int64_t f : factors)
+    if (f < 0 || __builtin_mul_overflow(p, f, &p)) return false;
+  return p < limit;
+}
+
+// Rows 0 .. rows-1 of `width` elements at `stride` elements per row span
+// fewer than 2^31 bytes (31-bit offsets inside the kernels). rows < 2^30.
+inline bool span_below_2g(int64_t rows, int64_t stride, int64_t width, int elt) {
+  if (stride < 0 || stride >= (int64_t(1) << 31)) return false;
+  return ((rows - 1) * stride + width) * elt < (int64_t(1) << 31);
+}
 
 // Row starts of a strided view are 16-byte aligned when the base is and every
 // outer stride is a multiple of 16 bytes.
