@@ -470,6 +470,24 @@ def cpu_baseline_attn_core(repeats: int):
     }
 
 
+def git_record() -> dict:
+    """The repository's commit when it has one here; otherwise (a copy of the
+    tree without history) the commit the in-tree library was built at, with
+    whether the kernel sources still match that build."""
+    rec = collect_git(ROOT)
+    if rec.get("commit"):
+        return rec
+    from techjam_amd import build as tj_build
+
+    try:
+        info = json.loads(tj_build.BUILD_INFO.read_text())
+    except (OSError, ValueError):
+        return rec
+    return {"commit": info.get("commit"), "dirty": info.get("library_sources_dirty"), "status": "",
+            "source": "library build record",
+            "library_sources_match": info.get("library_source_digest") == tj_build.library_source_digest()}
+
+
 def source_digest() -> str:
     """sha256 (16 hex digits) of the kernel sources, the C header and this file."""
     h = hashlib.sha256()
@@ -548,7 +566,7 @@ def main():
         "encoders": models_rec,
         "wall_s_timed_region": head["wall_s_timed_region"],
         "seeds": w.seeds,
-        "git": collect_git(ROOT),
+        "git": git_record(),
         "source_digest": source_digest(),
         "environment": collect_environment(torch, dev),
         "gpu_state": gpu_state,

@@ -7,6 +7,8 @@ shared library exposing the C ABI of ``include/techjam_attn.h``. Run as
 
 from __future__ import annotations
 
+import hashlib
+import json
 import os
 import shutil
 import subprocess
@@ -21,6 +23,9 @@ INCLUDE = ROOT / "include"
 LIBDIR = PKG / "lib"
 LIBNAME = "libtechjam_attn.so"
 OBJDIR = PKG / "_build"
+# Written next to the library: the commit and sources it was built from, so
+# that a run on a machine without the repository's history can still name them.
+BUILD_INFO = LIBDIR / "build_info.json"
 
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -48,6 +53,32 @@ def sources():
     return sorted(CSRC.glob("*.hip"))
 
 
+def library_source_digest() -> str:
+    """sha256 (16 hex digits) of everything the library is compiled from:
+    ``csrc/*`` (kernels and the shared header) and ``include/*.h``."""
+    h = hashlib.sha256()
+    for f in sorted(CSRC.glob("*")) + sorted(INCLUDE.glob("*.h")):
+        h.update(f.name.encode())
+        h.update(f.read_bytes())
+    return h.hexdigest()[:16]
+
+
+def _git(*args: str):
+    try:
+        res = subprocess.run(["git", "-C", str(ROOT), *args], capture_output=True, text=True, timeout=10)
+    except (OSError, subprocess.SubprocessError):
+        return None
+    return res.stdout.strip() if res.returncode == 0 else None
+
+
+def write_build_info() -> dict:
+    commit = _git("rev-parse", "HEAD")
+    status = _git("status", "--short", "--", "techjam_amd/csrc", "include") if commit else None
+    info = {"commit": commit, "library_sources_dirty": bool(status), "library_source_digest": library_source_digest()}
+    BUILD_INFO.write_text(json.dumps(info, indent=1) + "\n")
+    return info
+
+
 def _compile(src: Path) -> Path:
     obj = OBJDIR / (src.stem + ".o")
     cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
@@ -73,6 +104,7 @@ def build(verbose: bool = False) -> Path:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, out)
+    write_build_info()
     if verbose:
         print(f"built {out}")
     return out

@@ -90,3 +90,21 @@ def test_bench_uses_the_oracle_only_for_the_cpu_baseline():
 def test_the_package_never_imports_the_oracle():
     for path in (ROOT / "techjam_amd").rglob("*.py"):
         assert not _oracle_imports(ast.parse(path.read_text())), path
+
+
+def test_bench_git_record_falls_back_to_the_library_build_record(monkeypatch, tmp_path):
+    """Without repository history (a copy of the tree) the record names the
+    commit the library was built at and whether its sources still match."""
+    import bench
+    from techjam_amd import build as tj_build
+
+    info = tmp_path / "build_info.json"
+    monkeypatch.setattr(tj_build, "BUILD_INFO", info)
+    monkeypatch.setattr(bench, "collect_git", lambda root=None: {"commit": None, "dirty": False, "status": ""})
+    assert bench.git_record()["commit"] is None  # no record either
+    info.write_text('{"commit": "abc123", "library_sources_dirty": false, "library_source_digest": "%s"}'
+                    % tj_build.library_source_digest())
+    rec = bench.git_record()
+    assert rec["commit"] == "abc123" and rec["library_sources_match"] is True
+    info.write_text('{"commit": "abc123", "library_sources_dirty": false, "library_source_digest": "0"}')
+    assert bench.git_record()["library_sources_match"] is False
