@@ -562,11 +562,13 @@ __device__ __forceinline__ void store_shadow_t(half_t* dst, const float16_t& acc
 }
 
 // The same block written into the piece-major quad shadow of S_i,
-// [8 q][64 v][8 j] (q = j / 8), as the apply's ring reads it.
-__device__ __forceinline__ void store_quad_shadow(half_t* dst, const float16_t& acc, int rb, int cb) {
+// [8 q][64 v][8 j] (q = j / 8), as the apply's ring reads it, from row group
+// g0 on (g0 = 2 skips j = 32 rb .. 32 rb + 15).
+__device__ __forceinline__ void store_quad_shadow(half_t* dst, const float16_t& acc, int rb, int cb, int g0) {
   const int lane = threadIdx.x % kWave, hl = lane / 32, ln = lane % 32;
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
+    if (g < g0) continue;
     const int j = 32 * rb + 8 * g + 4 * hl;  // four consecutive j, one piece
     *reinterpret_cast<half4_t*>(dst + ((j >> 3) * 64 + 32 * cb + ln) * 8 + (j & 7)) =
         half4_t{(half_t)acc[4 * g], (half_t)acc[4 * g + 1], (half_t)acc[4 * g + 2], (half_t)acc[4 * g + 3]};
@@ -627,7 +629,10 @@ __device__ __forceinline__ void quad_update_body(const PolyArgs& a, char* ws, in
         }
       },
       [&](int j) {
-        // fp16 shadow of state_{c+1} for the applies of the next launch.
+        // fp16 shadow of state_{c+1} for the applies of the next launch: only
+        // the pieces the apply reads. For i in 16..31 and 48..63 it skips the
+        // 16 columns j below i's own 16-block (S is symmetric), which are the
+        // first half of this wave's first j-block.
         const int c = c0 + j;
         half_t* sh = reinterpret_cast<half_t*>(ws + kQuadShadow) + size_t((c + 1) % NSLOT) * PD * PD * PD;
 #pragma unroll
@@ -636,7 +641,8 @@ __device__ __forceinline__ void quad_update_body(const PolyArgs& a, char* ws, in
           for (int jj = 0; jj < NJ; ++jj)
 #pragma unroll
             for (int vb = 0; vb < 2; ++vb)
-              store_quad_shadow(sh + size_t(i0 + ii) * PD * PD, acc[ii][jj][vb], JB0 + jj, vb);
+              store_quad_shadow(sh + size_t(i0 + ii) * PD * PD, acc[ii][jj][vb], JB0 + jj, vb,
+                                jj == 0 && ((i0 + ii) & 16) ? 2 : 0);
       });
 #pragma unroll
   for (int ii = 0; ii < NI; ++ii)
