@@ -261,3 +261,74 @@ def test_full_benchmark_shape_every_head(cuda):
         torch.set_float32_matmul_precision(prev)
     print(f"attention core, all 1024 heads: failed={failed} max_abs={max_abs:.3e}")
     assert failed == 0 and max_abs <= 4e-3
+
+
+def _sweep_cases(n, seed):
+    """Seeded random configurations: shape, head dim, causality, dtype,
+    layout ([B, S, H, D] storage viewed as [B, H, S, D], or contiguous), valid
+    lengths (0 and S included), split scores."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        b, h = int(rng.integers(1, 5)), int(rng.integers(1, 6))
+        s = int(rng.choice([1, 2, 63, 64, 65, 127, 255, 256, 257, 511, 700, 1024, 1500]))
+        d = int(rng.choice([32, 64, 128]))
+        lengths = None
+        if rng.random() < 0.6:
+            lengths = [int(x) for x in rng.integers(0, s + 1, size=b)]
+            lengths[int(rng.integers(0, b))] = s
+        cases.append(dict(b=b, h=h, s=s, d=d, causal=bool(rng.random() < 0.6), lengths=lengths,
+                          f16=bool(rng.random() < 0.3), bshd=bool(rng.random() < 0.5),
+                          split=bool(rng.random() < 0.25), seed=1000 + i))
+    return cases
+
+
+@pytest.mark.parametrize("case", _sweep_cases(40, 2024), ids=lambda c: "{seed}-b{b}h{h}s{s}d{d}{}{}{}{}".format(
+    "c" if c["causal"] else "", "L" if c["lengths"] else "", "h" if c["f16"] else "", "x" if c["split"] else "",
+    **c))
+def test_random_configurations_match_brute_force(cuda, case):
+    """Every combination the dispatcher can hand the kernel, against the
+    float64 brute force; ``out`` starts as NaN so an unwritten row fails."""
+    from techjam_amd.kernels import scaled_dot_product_attention
+
+    b, h, s, d = case["b"], case["h"], case["s"], case["d"]
+    dt = torch.float16 if case["f16"] else torch.float32
+    q, k, v = (_draw((b, s, h, d), case["seed"] + j, dtype=dt) for j in range(3))
+    if case["bshd"]:
+        views = [t.to(cuda).transpose(1, 2) for t in (q, k, v)]
+        out = torch.full((b, s, h, d), float("nan"), device=cuda, dtype=dt).transpose(1, 2)
+    else:
+        views = [t.transpose(1, 2).contiguous().to(cuda) for t in (q, k, v)]
+        out = torch.full((b, h, s, d), float("nan"), device=cuda, dtype=dt)
+    vl = None if case["lengths"] is None else torch.tensor(case["lengths"], dtype=torch.int32, device=cuda)
+    scaled_dot_product_attention(*views, is_causal=case["causal"], valid_len=vl, out=out,
+                                 qk_split=True if case["split"] else None)
+    torch.cuda.synchronize()
+    ref = brute_force_attention(*(t.cpu() for t in views), d ** -0.5, case["causal"], valid_len=case["lengths"])
+    _assert_close(out.float(), ref, max_abs=4e-3 if not case["f16"] else 6e-3, what=str(case))
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_wide_tiles_with_ragged_lengths(cuda, causal):
+    """B=8 H=16 S=2048 takes the 256-row tile path (1024 wide tiles) with
+    right padding: every (b, h) against the blockwise oracle on the GPU."""
+    from techjam_amd.kernels import scaled_dot_product_attention
+
+    b, s, h, d = 8, 2048, 16, 64
+    g = torch.Generator(device=cuda).manual_seed(77)
+    q, k, v = (torch.randn(b, s, h, d, generator=g, device=cuda).transpose(1, 2) for _ in range(3))
+    lengths = torch.tensor([2048, 1, 0, 257, 1024, 2047, 700, 1500], dtype=torch.int32, device=cuda)
+    out = torch.full((b, s, h, d), float("nan"), device=cuda).transpose(1, 2)
+    scaled_dot_product_attention(q, k, v, is_causal=causal, valid_len=lengths, out=out)
+    torch.cuda.synchronize()
+    prev = torch.get_float32_matmul_precision()
+    torch.set_float32_matmul_precision("highest")
+    try:
+        ref = blockwise_attention(q, k, v, d ** -0.5, causal, valid_len=lengths, block_q=512, block_k=512)
+    finally:
+        torch.set_float32_matmul_precision(prev)
+    err = (out - ref).abs()
+    ok = torch.isfinite(out) & ((err <= ATOL) | (err <= RTOL * ref.abs()))
+    assert int((~ok).sum()) == 0, f"{int((~ok).sum())} failing, max abs {float(err.max()):.3e}"
+    for bi, n in enumerate(lengths.tolist()):
+        assert torch.count_nonzero(out[bi, :, n:]).item() == 0
