@@ -16,6 +16,7 @@ Three levels:
 
 from __future__ import annotations
 
+import numpy as np
 import pytest
 import torch
 
@@ -206,3 +207,54 @@ def test_extreme_length_workload_against_linear_memory_oracle(cuda):
         del ref
     print(f"extreme length: peak={peak / 2**30:.2f} GiB max_abs={mx:.3e} failed={failed}")
     assert failed == 0
+
+
+def _guard_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        b, h = int(rng.integers(1, 4)), int(rng.integers(1, 6))
+        s = int(rng.choice([4097, 4608, 5000, 6144, 8192 + 77, 10240, 12288 + 5]))
+        # per-head input std: score sigma = std^2 (D = 64), so 0.3 and 0.5
+        # take the polynomial route, 1.0 and 2.0 the exact fallback
+        stds = [float(x) for x in rng.choice([0.3, 0.5, 1.0, 2.0], size=h)]
+        cases.append(dict(b=b, h=h, s=s, stds=stds, layout=str(rng.choice(["bhsd", "bshd", "packed"])),
+                          f16=bool(rng.random() < 0.3), seed=500 + i))
+    return cases
+
+
+@pytest.mark.parametrize("case", _guard_cases(12, 7), ids=lambda c: "{seed}-b{b}h{h}s{s}-{layout}{}".format(
+    "-f16" if c["f16"] else "", **c))
+def test_guarded_route_random_configurations(cuda, case):
+    """Seeded shapes past the exact prefix (ragged tails included), mixed
+    per-head score ranges, three memory layouts and both input types, against
+    exact attention in fp32 on the GPU: the guard's routing and zero OR-rule
+    failures over every element."""
+    from techjam_amd.implementations.poly_attention import guarded_attention
+
+    b, h, s, d = case["b"], case["h"], case["s"], 64
+    dt = torch.float16 if case["f16"] else torch.float32
+    g = torch.Generator(device=cuda).manual_seed(case["seed"])
+    std = torch.tensor(case["stds"], device=cuda).view(1, h, 1, 1)
+    if case["layout"] == "packed":
+        qkv = torch.randn(b, s, 3, h, d, generator=g, device=cuda)
+        q, k, v = (qkv[:, :, j].transpose(1, 2) for j in range(3))
+    elif case["layout"] == "bshd":
+        q, k, v = (torch.randn(b, s, h, d, generator=g, device=cuda).transpose(1, 2) for _ in range(3))
+    else:
+        q, k, v = (torch.randn(b, h, s, d, generator=g, device=cuda) for _ in range(3))
+    q, k = (q * std).to(dt), (k * std).to(dt)
+    v = v.to(dt)
+    out, gr = guarded_attention(q, k, v, d ** -0.5)
+    prev = torch.get_float32_matmul_precision()
+    torch.set_float32_matmul_precision("highest")
+    try:
+        ref = blockwise_attention(q.float(), k.float(), v.float(), d ** -0.5, True, block_q=2048, block_k=2048)
+    finally:
+        torch.set_float32_matmul_precision(prev)
+    torch.cuda.synchronize()
+    want_flags = [int(x <= 0.5) for x in case["stds"]] * b
+    assert gr.flags.cpu().tolist() == want_flags
+    bad, mx = _or_failures(out.float(), ref)
+    print(f"{case}: max_abs={mx:.2e} failed={bad}")
+    assert bad == 0
