@@ -507,7 +507,7 @@ BUILDERS = {"attn-core": attn_core, "extreme": extreme, "copy-1gib": copy_1gib,
 def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
+        print("bench.py measures one GPU only: the library has no multi-GPU path "
               "(each (b, h) is independent; see the sharding notes)", file=sys.stderr)
         return 2
     if not torch.cuda.is_available():

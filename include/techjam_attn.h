@@ -36,7 +36,7 @@ extern "C" {
 #define TJ_ERR_SHAPE 1       /* inconsistent or non-positive sizes            */
 #define TJ_ERR_DTYPE 2       /* unsupported element type                      */
 #define TJ_ERR_ALIGN 3       /* pointer/stride not aligned for vector access  */
-#define TJ_ERR_UNSUPPORTED 4 /* valid request this build does not implement   */
+#define TJ_ERR_UNSUPPORTED 4 /* valid request the library does not implement */
 #define TJ_ERR_LAUNCH 5      /* the HIP runtime rejected a launch             */
 #define TJ_ERR_WORKSPACE 6   /* workspace missing or too small                */
 #define TJ_ERR_SCRATCH 7     /* request larger than a fixed library scratch   */

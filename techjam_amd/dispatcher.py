@@ -14,8 +14,8 @@ Keeps the public interface of the reference's ``src/dispatcher.py:39-818`` --
   allocation, and a failing kernel call is recorded in ``compile_failures``
   and re-raised;
 * routes are keyed by the reference's 7-tuple ``(B, S, d_model, H, ffn, causal,
-  layers)``: the fourteen disclosed cases plus this build's benchmark model
-  configurations; shapes outside the table take the generic exact route
+  layers)``: the fourteen disclosed cases plus the five benchmark model
+  configurations (C1-C5); shapes outside the table take the generic exact route
   (the kernels are shape-generic);
 * a right-padded mask is classified once per tensor and version (one host
   synchronisation, ``src/dispatcher.py:393-423``) and turned into device-side

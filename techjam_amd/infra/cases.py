@@ -1,9 +1,9 @@
-"""Case tables: the reference's fourteen disclosed shapes and this build's five workloads.
+"""Case tables: the reference's fourteen disclosed shapes and the five benchmark workloads.
 
 ``OFFICIAL_CASES`` holds the organiser's shape table that the reference keeps
 in ``src/cases/task_shapes.json`` (loaded by ``src/infra/cases.py:54-71``); the
 values are data the route table must key on, so they are the same.
-``BENCHMARK_CONFIGS`` are the five configurations this build is measured on.
+``BENCHMARK_CONFIGS`` are the five benchmark configurations (C1-C5) the kernels are measured on.
 """
 
 from __future__ import annotations
