@@ -30,7 +30,7 @@ HOST_SANITIZE = ("-Xarch_host -fsanitize=address -Xarch_host -fsanitize=undefine
 
 
 @pytest.fixture(scope="module")
-def checker(tmp_path_factory) -> Path:
+def abi_checks_exe(tmp_path_factory) -> Path:
     if not (Path(HIPCC).exists() and Path(CLANG).exists()):
         pytest.skip("ROCm compilers not found")
     out = tmp_path_factory.mktemp("sanitize")
@@ -60,11 +60,11 @@ def checker(tmp_path_factory) -> Path:
     return exe
 
 
-def test_argument_checks_under_asan_and_ubsan(checker):
+def test_argument_checks_under_asan_and_ubsan(abi_checks_exe):
     env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=0",
                UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1",
                HIP_VISIBLE_DEVICES="")  # the checks must not need a device
-    res = subprocess.run([str(checker)], capture_output=True, text=True, env=env, timeout=120)
+    res = subprocess.run([str(abi_checks_exe)], capture_output=True, text=True, env=env, timeout=120)
     report = res.stdout + res.stderr
     assert "runtime error" not in report and "AddressSanitizer" not in report, report[-4000:]
     assert res.returncode == 0, report[-4000:]
