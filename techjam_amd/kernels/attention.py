@@ -47,15 +47,30 @@ def _require_device(*tensors: torch.Tensor) -> torch.device:
     return dev
 
 
-def _kernel_view(t: torch.Tensor) -> torch.Tensor:
+#: The kernels address the rows of one (b, h) with 31-bit byte offsets.
+MAX_HEAD_SPAN_BYTES = 1 << 31
+
+
+def _head_span_bytes(t: torch.Tensor) -> int:
+    s, d = t.shape[2], t.shape[3]
+    return ((s - 1) * t.stride(2) + d) * t.element_size() if s > 0 else 0
+
+
+def _kernel_view(t: torch.Tensor, keys: bool = False) -> torch.Tensor:
     """``t`` itself when the kernels can read it in place, else a contiguous copy.
 
     In-place reading needs a unit innermost stride, 16-byte aligned rows and a
-    16-byte aligned base; the model's projection views always qualify.
+    16-byte aligned base, and for keys and values (``keys``) rows of one
+    (b, h) spanning under 2 GiB; the model's projection views qualify. The
+    copy is ``[B, H, S, D]`` contiguous, whose head span is ``S*D`` elements
+    -- so keys of a long sequence in an interleaved ``[B, S, H, D]`` layout
+    (over 2^31 / (H*D*4) tokens in fp32) cost one copy instead of being
+    refused.
     """
     vec = 16 // t.element_size()
     st = t.stride()
-    if st[3] == 1 and all(s % vec == 0 for s in st[:3]) and t.data_ptr() % 16 == 0:
+    if (st[3] == 1 and all(s % vec == 0 for s in st[:3]) and t.data_ptr() % 16 == 0
+            and (not keys or (st[2] >= 0 and _head_span_bytes(t) < MAX_HEAD_SPAN_BYTES))):
         return t
     return t.contiguous()
 
@@ -146,7 +161,7 @@ def scaled_dot_product_attention(
         res = scaled_dot_product_attention(q, k, v, is_causal=is_causal, scale=scale, valid_len=valid_len,
                                            row_limit=row_limit, qk_split=qk_split, q_bias=q_bias, v_bias=v_bias)
         return res[..., :d]
-    q, k, v = _kernel_view(q), _kernel_view(k), _kernel_view(v)
+    q, k, v = _kernel_view(q), _kernel_view(k, keys=True), _kernel_view(v, keys=True)
     if out is None:
         out = empty_like_heads(q)
     elif out.shape != q.shape or out.dtype != q.dtype or out.device != dev:

@@ -46,7 +46,7 @@ def poly_rows(
         raise ValueError("out must match q in shape, dtype and device")
     dev = _require_device(q, k, v)
     b, h, s, d = q.shape
-    q, k, v = _kernel_view(q), _kernel_view(k), _kernel_view(v)
+    q, k, v = _kernel_view(q), _kernel_view(k, keys=True), _kernel_view(v, keys=True)
     if out is None:
         out = empty_like_heads(q)
     m = b * h

@@ -332,3 +332,27 @@ def test_wide_tiles_with_ragged_lengths(cuda, causal):
     assert int((~ok).sum()) == 0, f"{int((~ok).sum())} failing, max abs {float(err.max()):.3e}"
     for bi, n in enumerate(lengths.tolist()):
         assert torch.count_nonzero(out[bi, :, n:]).item() == 0
+
+
+def test_keys_spanning_more_than_2_gib_are_copied_not_refused(cuda):
+    """k and v rows 4 MiB apart (600 rows span 2.3 GiB, beyond the kernels'
+    31-bit offsets): the wrapper reads them through a contiguous copy, and the
+    result is bitwise that of contiguous inputs."""
+    from techjam_amd.kernels import scaled_dot_product_attention
+
+    b, h, s, d, row = 1, 2, 600, 64, 1 << 20
+    g = torch.Generator(device=cuda).manual_seed(9)
+    q = torch.randn(b, h, s, d, generator=g, device=cuda)
+    big_k = torch.zeros(s, row, device=cuda)
+    big_v = torch.zeros(s, row, device=cuda)
+    big_k[:, : h * d] = torch.randn(s, h * d, generator=g, device=cuda)
+    big_v[:, : h * d] = torch.randn(s, h * d, generator=g, device=cuda)
+    k = big_k[:, : h * d].view(s, h, d).unsqueeze(0).transpose(1, 2)  # [1, H, S, D], row stride 2^20
+    v = big_v[:, : h * d].view(s, h, d).unsqueeze(0).transpose(1, 2)
+    assert ((s - 1) * k.stride(2) + d) * 4 >= 1 << 31
+    got = scaled_dot_product_attention(q, k, v, is_causal=True)
+    want = scaled_dot_product_attention(q, k.contiguous(), v.contiguous(), is_causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    del big_k, big_v, k, v
+    torch.cuda.empty_cache()

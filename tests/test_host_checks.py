@@ -66,3 +66,16 @@ def test_mask_lengths_follow_an_inference_mask_refilled_in_place():
         kind, lengths = cand._mask_info(mask)
         assert kind is MaskKind.PREFIX and lengths.tolist() == [2, 7]
         assert cand._mask_info(None) == (MaskKind.ABSENT, None)
+
+
+def test_head_span_rule_for_keys():
+    """Keys whose rows of one (b, h) span 2 GiB or more cannot be addressed in
+    place by the kernels (31-bit offsets): the wrapper copies them to a
+    [B, H, S, D]-contiguous layout, whose span is S*D elements."""
+    from techjam_amd.kernels.attention import MAX_HEAD_SPAN_BYTES, _head_span_bytes
+
+    b, h, s, d = 1, 16, 600_000, 64
+    bshd = torch.empty_strided((b, h, s, d), (s * h * d, d, h * d, 1), device="meta")  # [B, S, H, D] storage
+    assert _head_span_bytes(bshd) >= MAX_HEAD_SPAN_BYTES
+    assert _head_span_bytes(bshd.contiguous()) == s * d * 4 < MAX_HEAD_SPAN_BYTES
+    assert _head_span_bytes(torch.empty((1, 1, 0, 64), device="meta")) == 0
