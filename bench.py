@@ -72,7 +72,8 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--workload", default="attn-core",
                    choices=["attn-core", "extreme", "model-c1", "model-c2", "model-c4", "copy-1gib",
-                            "quad-apply", "quad-update", "causal-diag"])
+                            "quad-apply", "quad-update", "causal-diag", "core-100k-exact", "core-100k-poly"]
+                   + [f"case-{i}" for i in range(1, 15)])
     p.add_argument("--no-extreme", action="store_true",
                    help="with the default workload, skip the extreme-length measurement")
     p.add_argument("--no-accuracy", action="store_true", help="skip the sampled-heads accuracy check")
@@ -327,6 +328,88 @@ def model(name):
     return build
 
 
+# The reference's published candidate latencies on an RTX 5080, for context
+# beside the same shapes here (research/benchmarks/2026-08-31-rtx5080-775c820/
+# README.md:22-34 for cases 1-13; latest-dispatcher-case14.json: 67.095 s over
+# five full forwards of case 14; research/benchmarks/2026-08-30-rtx5080-b9506f3/
+# attention-core.json:37-39 for the attention core at N = 100 000).
+REFERENCE_RTX5080_MS = {
+    "case-1": 0.6975, "case-2": 0.1609, "case-3": 0.1643, "case-4": 0.2678, "case-5": 1.2513,
+    "case-6": 210.5723, "case-7": 0.4060, "case-8": 15.5889, "case-9": 0.6881, "case-10": 0.6464,
+    "case-11": 1.3724, "case-12": 0.2335, "case-13": 13.6078, "case-14": 67094.5 / 5,
+    "core-100k-exact": 200.006, "core-100k-poly": 128.104,
+}
+
+
+def official_case(case_id: int):
+    """Whole-model forward of one of the fourteen official cases: the
+    dispatcher at the case's shape, default-initialised weights, the harness's
+    inputs without padding (its default), float32 GEMMs under its flags."""
+    def build(args, dev) -> Workload:
+        from techjam_amd.dispatcher import DispatchingTransformer
+        from techjam_amd.infra import load_official_cases
+        from techjam_amd.model import TransformerConfig
+
+        c = load_official_cases()[case_id]
+        cfg = TransformerConfig(c.batch_size, c.seq_len, c.qkv_dim, c.heads, c.ffn_dim, c.layers, c.causal)
+        torch.manual_seed(1234)
+        cand = DispatchingTransformer(cfg).eval().to(dev)
+        x, mask = random_case(c.batch_size, c.seq_len, c.qkv_dim, TIMING_SEED, 0.0, 1.0, device=dev)
+        torch.set_float32_matmul_precision(args.matmul_precision)
+        torch.backends.cuda.matmul.allow_tf32 = args.allow_tf32
+
+        def step():
+            with torch.inference_mode():
+                cand(x, mask)
+
+        hd = c.qkv_dim // c.heads
+        config = {"workload": f"official case {case_id}: {c.layers}-layer encoder, B={c.batch_size} "
+                              f"S={c.seq_len} d_model={c.qkv_dim} H={c.heads} FFN={c.ffn_dim}, causal",
+                  "batch": c.batch_size, "seq_len": c.seq_len, "d_model": c.qkv_dim, "heads": c.heads,
+                  "ffn_dim": c.ffn_dim, "layers": c.layers,
+                  "reference_rtx5080_ms": REFERENCE_RTX5080_MS[f"case-{case_id}"],
+                  "roofline_scope": "exact attention FLOPs over the whole forward (GEMMs not counted)",
+                  "gemm": f"fp32 tensors, matmul precision {args.matmul_precision!r}, allow_tf32={args.allow_tf32}"}
+        return Workload(step, c.batch_size * c.seq_len,
+                        c.layers * exact_attention_flops([c.seq_len] * c.batch_size, c.heads, hd), 0.0, config,
+                        f"case_{case_id}.md", data="synthetic: x ~ N(0, 1), no padding (seed 101234, generated on "
+                        "the GPU), default-initialised weights (seed 1234)",
+                        seeds={"timing_input": TIMING_SEED, "weights": 1234})
+    return build
+
+
+def core_100k(route: str):
+    """The reference's attention-core benchmark shape (src/bench_poly.py:194-233):
+    B=1, N=100 000, H=16, d=64, fp16 q, k, v ~ N(0, 0.577^2) as strided
+    [B, N, H, D] views, causal; ``exact`` is exact attention, ``poly`` the
+    polynomial path at the reference's fixed sigma 0.3338 (no guard)."""
+    def build(args, dev) -> Workload:
+        from techjam_amd.implementations.poly_attention import poly_attention_forward
+        from techjam_amd.kernels import scaled_dot_product_attention
+
+        b, n, h, d = 1, 100_000, 16, 64
+        g = torch.Generator(device=dev).manual_seed(0)
+        packed = [(torch.randn(b, n, h * d, generator=g, device=dev) * 0.577).half() for _ in range(3)]
+        q, k, v = (t.view(b, n, h, d).transpose(1, 2) for t in packed)
+        scale = d ** -0.5
+
+        def step():
+            with torch.inference_mode():
+                if route == "exact":
+                    scaled_dot_product_attention(q, k, v, is_causal=True, scale=scale)
+                else:
+                    poly_attention_forward(q, k, v, scale, sigma=0.3338)
+
+        flops = (exact_attention_flops([n], h, d) if route == "exact" else h * poly_flops(n, d, d, 512, 4096))
+        config = {"workload": f"attention core at the reference's benchmark shape, {route}: B=1 N=100000 H=16 "
+                              "d=64, fp16, causal",
+                  "batch": b, "seq_len": n, "heads": h, "head_dim": d,
+                  "reference_rtx5080_ms": REFERENCE_RTX5080_MS[f"core-100k-{route}"]}
+        return Workload(step, b * n, flops, attention_bytes(b, n, h, d, 2), config, f"core_100k_{route}.md",
+                        data="synthetic: q, k, v ~ N(0, 0.577^2) fp16 (seed 0, generated on the GPU)")
+    return build
+
+
 BENCHMARK_CONFIG_TEXT = {
     "C2": "4-layer encoder, B=8 S=1024 d_model=512 H=8 FFN=2048, packed QKV, causal, right padding",
     "C4": "4-layer encoder, B=2 S=8192 d_model=1024 H=16 FFN=4096, causal, right padding",
@@ -501,7 +584,9 @@ def source_digest() -> str:
 BUILDERS = {"attn-core": attn_core, "extreme": extreme, "copy-1gib": copy_1gib,
             "quad-apply": poly_part("quad-apply"), "quad-update": poly_part("quad-update"),
             "causal-diag": poly_part("causal-diag"),
-            "model-c1": model("C1"), "model-c2": model("C2"), "model-c4": model("C4")}
+            "model-c1": model("C1"), "model-c2": model("C2"), "model-c4": model("C4"),
+            "core-100k-exact": core_100k("exact"), "core-100k-poly": core_100k("poly"),
+            **{f"case-{i}": official_case(i) for i in range(1, 15)}}
 
 
 def main():

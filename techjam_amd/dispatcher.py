@@ -81,10 +81,12 @@ BENCHMARK_CASE_BY_CONFIG: Dict[ConfigKey, str] = {
 }
 PACKED_QKV_CASES = frozenset((2, 3, "C2", "C4"))
 EXTREME_CASES = (6, 14)
-# Launch-bound sizes replayed as HIP graphs (C1: 256 tokens; C2's 8192 and
-# C4's 16384 tokens are kernel-bound and gain nothing), and captures kept per
-# model.
-GRAPH_MAX_TOKENS = 4096
+# Launch-bound sizes replayed as HIP graphs, by input elements (tokens x
+# d_model): C1 (256 x 256) and the official cases of 128-token sequences up to
+# 128 x 128 x 128 are launch-bound; C2 (8192 x 512), C4 and cases 8 and 13
+# (8192 x 1024, 65536 x 128) are kernel-bound and gain nothing. Captures are
+# kept per model.
+GRAPH_MAX_ELEMENTS = 1 << 21
 GRAPH_CACHE_SIZE = 8
 
 
@@ -177,7 +179,7 @@ class DispatchingTransformer(TransformerEncoder):
     """Lazy per-instance dispatcher whose attention always runs the HIP kernels."""
 
     #: Replay the exact-attention forward as a HIP graph for inputs of at most
-    #: ``GRAPH_MAX_TOKENS`` tokens (inference only); ``TECHJAM_AMD_GRAPHS=0``
+    #: ``GRAPH_MAX_ELEMENTS`` input elements (inference only); ``TECHJAM_AMD_GRAPHS=0``
     #: in the environment turns it off.
     use_graphs = True
     #: Device bytes the streamed routes (cases 6 and 14) may plan for; None
@@ -306,7 +308,7 @@ class DispatchingTransformer(TransformerEncoder):
         return (self.use_graphs and os.environ.get("TECHJAM_AMD_GRAPHS", "1") != "0"
                 and x.is_cuda and x.device.index == torch.cuda.current_device()
                 and x.ndim == 3 and x.is_contiguous() and not torch.is_grad_enabled()
-                and x.shape[0] * x.shape[1] <= GRAPH_MAX_TOKENS
+                and x.numel() <= GRAPH_MAX_ELEMENTS
                 and not torch.cuda.is_current_stream_capturing())
 
     def _forward_graphed(self, x, mask, lengths):

@@ -18,6 +18,7 @@ pytestmark = pytest.mark.gpu
 
 C1 = OracleConfig(2, 128, 256, 4, 1024, 1, True)
 C2 = OracleConfig(8, 1024, 512, 8, 2048, 4, True)
+CASE5 = OracleConfig(128, 128, 128, 4, 128, 4, True)  # official case 5: 16384 tokens, replayed by default
 
 
 def _model(cfg, seed, cuda):
@@ -43,12 +44,12 @@ def _eager(model, x, mask):
         model.use_graphs = True
 
 
-@pytest.mark.parametrize("cfg,operands", [(C1, "fp32"), (C2, "fp32"), (C2, "fp16")],
-                         ids=["C1", "C2", "C2-fp16-operands"])
+@pytest.mark.parametrize("cfg,operands", [(C1, "fp32"), (C2, "fp32"), (C2, "fp16"), (CASE5, "fp32")],
+                         ids=["C1", "C2", "C2-fp16-operands", "case5"])
 def test_every_replay_matches_eager(cuda, cfg, operands, monkeypatch):
     from techjam_amd import dispatcher as D
 
-    monkeypatch.setattr(D, "GRAPH_MAX_TOKENS", 8192)   # C2 runs eagerly by default
+    monkeypatch.setattr(D, "GRAPH_MAX_ELEMENTS", 8192 * 512)   # C2 runs eagerly by default
     model = _model(cfg, 11, cuda)
     model.gemm_operands = operands
     inputs = [_inputs(cfg, 1234 + i, cuda) for i in range(4)]
@@ -111,11 +112,11 @@ def test_graph_replay_is_off_for_large_inputs_and_by_environment(cuda, monkeypat
 
     model = _model(C1, 5, cuda)
     x, mask = _inputs(C1, 7, cuda)
-    monkeypatch.setattr(D, "GRAPH_MAX_TOKENS", 128)
+    monkeypatch.setattr(D, "GRAPH_MAX_ELEMENTS", 128)
     with torch.inference_mode():
         model(x, mask)
     assert not model._graphs
-    monkeypatch.setattr(D, "GRAPH_MAX_TOKENS", 4096)
+    monkeypatch.setattr(D, "GRAPH_MAX_ELEMENTS", 1 << 21)
     monkeypatch.setenv("TECHJAM_AMD_GRAPHS", "0")
     with torch.inference_mode():
         model(x, mask)
