@@ -185,6 +185,11 @@ class DispatchingTransformer(TransformerEncoder):
     #: Device bytes the streamed routes (cases 6 and 14) may plan for; None
     #: takes 85 % of the device less what is already allocated.
     memory_budget_bytes: Optional[int] = None
+    #: GEMM operands of the case-14 route. The reference computes that case in
+    #: fp16 behind its fp32 interface (src/dispatcher.py:488-518: fp16
+    #: residual stream, autocast fp16 GEMMs); "fp16" here rounds the GEMM
+    #: operands only, with fp32 accumulation, residual stream and norms.
+    case14_gemm_operands = "fp16"
 
     def __init__(self, config: TransformerConfig) -> None:
         super().__init__(config)
@@ -355,7 +360,7 @@ class DispatchingTransformer(TransformerEncoder):
             raise UnsupportedCaseError("case 14 chunks require float16 or float32 GPU input")
         if valid_token_mask is not None:
             raise ValueError("trim padding before the case 14 chunk")
-        return self.forward_layers(x, None, None)
+        return self.forward_layers(x, None, None, gemm_operands=self.case14_gemm_operands)
 
     def _forward_case_14(self, x, valid_token_mask=None):
         chunk = self._plan_chunk(x, poly=True)

@@ -23,8 +23,10 @@ from collections.abc import Callable
 from typing import Optional
 
 import torch
+import torch.nn.functional as F
 
 from ..kernels.attention import scaled_dot_product_attention
+from ..model import fp16_weight
 from .poly_attention import guarded_attention
 from .poly_guard import poly_is_safe
 from .sdpa import StridedSDPASelfAttention
@@ -156,10 +158,23 @@ class ExactOnlySelfAttention(StridedSDPASelfAttention):
         if valid_token_mask is not None:
             raise ValueError("trim padding before calling extreme attention")
 
+    def qkv(self, x):
+        """q, k, v head views. An fp16 ``x`` (the fp16-operand layer stack)
+        runs each projection as one fp16 GEMM with its bias in the epilogue
+        (the parameters' cached fp16 copies, fp32 accumulation) and returns
+        fp16 q, k, v -- the reference's fp16 case-14 contract."""
+        if x.dtype != torch.float16:
+            return self.project_qkv(x)
+        out = []
+        for lin in (self.q_proj, self.k_proj, self.v_proj):
+            bias = None if lin.bias is None else fp16_weight(lin, "bias", lin.bias)
+            out.append(self.heads_view(F.linear(x, fp16_weight(lin, "weight", lin.weight), bias)))
+        return tuple(out)
+
     def context(self, x, valid_token_mask=None, causal=False, valid_len=None):
         self._check(x, valid_token_mask)
         b, s, _ = x.shape
-        q, k, v = self.project_qkv(x)
+        q, k, v = self.qkv(x)
         ctx = scaled_dot_product_attention(q, k, v, is_causal=causal, scale=self.scale)
         return ctx.transpose(1, 2).reshape(b, s, self.d_model)
 
@@ -185,6 +200,6 @@ class PolyOrExactSelfAttention(ExactOnlySelfAttention):
         if not causal:
             raise ValueError("the polynomial route is causal attention")
         b, s, _ = x.shape
-        q, k, v = self.project_qkv(x)
+        q, k, v = self.qkv(x)
         ctx, self.last_guard = guarded_attention(q, k, v, self.scale, enabled=self.poly_enabled)
         return ctx.transpose(1, 2).reshape(b, s, self.d_model)

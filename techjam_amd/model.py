@@ -377,12 +377,15 @@ class TransformerEncoder(nn.Module):
         # with norm=None); only the pre-norm stack has a final LayerNorm.
         self.final_norm = nn.LayerNorm(config.d_model) if self.norm_first else nn.Identity()
 
-    def forward_layers(self, x, valid_token_mask=None, valid_len=None):
-        if self.gemm_operands not in ("fp32", "fp16"):
-            raise ValueError(f"gemm_operands must be 'fp32' or 'fp16', not {self.gemm_operands!r}")
+    def forward_layers(self, x, valid_token_mask=None, valid_len=None, gemm_operands=None):
+        """The layer stack and final norm; ``gemm_operands`` overrides the
+        model's setting for this call."""
+        operands = self.gemm_operands if gemm_operands is None else gemm_operands
+        if operands not in ("fp32", "fp16"):
+            raise ValueError(f"gemm_operands must be 'fp32' or 'fp16', not {operands!r}")
         if self._can_fuse_norms(x, valid_token_mask, valid_len):
-            return self._forward_layers_fused(x, valid_token_mask, valid_len)
-        if self.gemm_operands == "fp16":
+            return self._forward_layers_fused(x, valid_token_mask, valid_len, operands)
+        if operands == "fp16":
             from .errors import UnsupportedCaseError
 
             raise UnsupportedCaseError("fp16 GEMM operands are implemented on the fused pre-norm GPU path only")
@@ -405,7 +408,7 @@ class TransformerEncoder(nn.Module):
                 and all(type(n) is nn.LayerNorm and n.elementwise_affine and n.bias is not None
                         and n.weight.dtype == torch.float32 for n in norms))
 
-    def _forward_layers_fused(self, x, valid_token_mask, valid_len):
+    def _forward_layers_fused(self, x, valid_token_mask, valid_len, operands="fp32"):
         """The layer stack with every LayerNorm but the first fused into the
         residual pass before it (same computation as the loop above)."""
         state = [x, self.layers[0].norm1(x)]
@@ -414,7 +417,7 @@ class TransformerEncoder(nn.Module):
         for i, layer in enumerate(self.layers):
             nxt = self.layers[i + 1].norm1 if i + 1 < n else self.final_norm
             state = list(layer._forward_fused_norms(state, valid_token_mask, self.config.causal, valid_len, nxt,
-                                                    last=i + 1 == n, fp16_operands=self.gemm_operands == "fp16"))
+                                                    last=i + 1 == n, fp16_operands=operands == "fp16"))
         return state[1]
 
     def forward(self, x, valid_token_mask: Optional[torch.Tensor] = None):

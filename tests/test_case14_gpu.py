@@ -67,10 +67,14 @@ def _poly_heads(cand) -> int:
     return sum(int(layer.attention.last_guard.flags.sum()) for layer in cand.layers)
 
 
-def test_streamed_sample_route_matches_linear_memory_oracle(cuda, case14_models):
+@pytest.mark.parametrize("operands", ["fp16", "fp32"])
+def test_streamed_sample_route_matches_linear_memory_oracle(cuda, case14_models, operands, monkeypatch):
+    """Both GEMM-operand contracts of the route: fp16 operands (the default,
+    the reference's fp16 case-14 compute) and fp32."""
     from techjam_amd.implementations.extreme import PolyOrExactSelfAttention
 
     oracle, cand = case14_models
+    monkeypatch.setattr(cand, "case14_gemm_operands", operands)
     assert all(type(layer.attention) is PolyOrExactSelfAttention for layer in cand.layers)
     x, mask = _input(1, 8192, [8192], 1234)
     x, mask = x.to(cuda), mask.to(cuda)
@@ -80,7 +84,8 @@ def test_streamed_sample_route_matches_linear_memory_oracle(cuda, case14_models)
         torch.cuda.synchronize()
     n_poly = _poly_heads(cand)
     res = compare_outputs_streamed(ref, got)
-    print(f"case 14 streamed sample, 8192 tokens: {n_poly}/32 heads polynomial, max_abs={res.max_abs_error:.3e} "
+    print(f"case 14 streamed sample ({operands} GEMM operands), 8192 tokens: {n_poly}/32 heads polynomial, "
+          f"max_abs={res.max_abs_error:.3e} "
           f"failed={res.failed_elements}/{res.total_elements}")
     assert n_poly > 0, "no head took the polynomial route"
     assert res.passed, f"{res.failed_elements} failing elements, max_abs {res.max_abs_error:.3e}"
