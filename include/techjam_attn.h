@@ -308,8 +308,8 @@ int tj_bias_relu(float* y, const float* bias, int64_t rows, int64_t cols, void* 
  * With zero_ln_padded, rows at or past valid_len get ln_out = 0 (the final
  * masked_fill). out may be NULL: the sum is then not stored, only its norm
  * (a post-norm block, whose residual stream is the norm of the sum). ln_out
- * must overlap none of out, x, y. cols must be 256, 512, 1024 or 2048
- * (TJ_ERR_UNSUPPORTED otherwise); all pointers 16-byte aligned.
+ * must overlap none of out, x, y. cols must be 32, 64, 128, 256, 512, 1024
+ * or 2048 (TJ_ERR_UNSUPPORTED otherwise); all pointers 16-byte aligned.
  */
 int tj_bias_residual_layernorm(float* out, void* ln_out, int ln_dtype, const float* x, const float* y,
                                const float* bias, const float* gamma, const float* beta,

@@ -141,6 +141,59 @@ __global__ __launch_bounds__(ET) void bias_residual_ln_kernel(float* out, TN* ln
 // byte counts of the operands fit 64 bits.
 constexpr int64_t kMaxElements = int64_t(1) << 56;
 
+// Rows of 32, 64 or 128 columns: LPR = cols / 4 lanes per row (one float4
+// each), 64 / LPR rows per wave, the mean and variance reduced over the row's
+// lane group with xor shuffles (offsets below LPR stay inside the group).
+// Same two exact passes as above.
+template <int LPR, typename TN>
+__global__ __launch_bounds__(ET) void bias_residual_ln_small_kernel(float* out, TN* ln_out, const float* x,
+                                                                    const float* y, const float* bias,
+                                                                    const float* gamma, const float* beta,
+                                                                    int64_t rows, int64_t seq_len,
+                                                                    const int32_t* valid_len, int mode, float eps,
+                                                                    int zero_ln_padded) {
+  constexpr int RPW = kWave / LPR;
+  const int lane = threadIdx.x % kWave;
+  const int c = lane % LPR;
+  const int64_t row = (blockIdx.x * (int64_t)(ET / kWave) + threadIdx.x / kWave) * RPW + lane / LPR;
+  const bool live = row < rows;  // every lane stays for the shuffles
+  const bool ok = live && (mode == 0 || row_valid(row, seq_len, valid_len));
+  float4_t r = {0.f, 0.f, 0.f, 0.f};
+  float sum = 0.f;
+  if (live) {
+    const float4_t xv = reinterpret_cast<const float4_t*>(x)[row * LPR + c];
+    const float4_t yv = reinterpret_cast<const float4_t*>(y)[row * LPR + c];
+    const float4_t bv = reinterpret_cast<const float4_t*>(bias)[c];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float t = yv[e] + bv[e];
+      r[e] = mode == 2 ? (ok ? xv[e] + t : 0.f) : xv[e] + (ok ? t : 0.f);
+      sum += r[e];
+    }
+    if (out != nullptr) reinterpret_cast<float4_t*>(out)[row * LPR + c] = r;
+  }
+#pragma unroll
+  for (int o = LPR / 2; o > 0; o >>= 1) sum += __shfl_xor(sum, o, kWave);
+  const float mean = sum / (float)(LPR * 4);
+  float sq = 0.f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float d = r[e] - mean;
+    sq += d * d;
+  }
+#pragma unroll
+  for (int o = LPR / 2; o > 0; o >>= 1) sq += __shfl_xor(sq, o, kWave);
+  if (!live) return;
+  const float rstd = 1.f / sqrtf(sq / (float)(LPR * 4) + eps);
+  const bool zero = zero_ln_padded != 0 && !row_valid(row, seq_len, valid_len);
+  const float4_t gv = reinterpret_cast<const float4_t*>(gamma)[c];
+  const float4_t hv = reinterpret_cast<const float4_t*>(beta)[c];
+  float4_t n;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) n[e] = zero ? 0.f : (r[e] - mean) * rstd * gv[e] + hv[e];
+  store4(ln_out, row * LPR + c, n);
+}
+
 unsigned grid_for(int64_t n4) {
   const int64_t blocks = (n4 + ET - 1) / ET;
   return (unsigned)(blocks < 256 * 32 ? blocks : 256 * 32);
@@ -205,6 +258,17 @@ template <typename TN>
 int launch_brl(float* out, TN* ln_out, const float* x, const float* y, const float* bias, const float* gamma,
                const float* beta, int64_t rows, int64_t cols, int64_t seq_len, const int32_t* vl, int mode, float eps,
                int zero_ln_padded, hipStream_t stream) {
+  if (cols < 256) {
+    const int64_t rows_per_block = (tj::ET / 64) * (64 / (cols / 4));
+    const dim3 sgrid((unsigned)((rows + rows_per_block - 1) / rows_per_block));
+    switch (cols) {
+      case 32: hipLaunchKernelGGL((tj::bias_residual_ln_small_kernel<8, TN>), sgrid, dim3(tj::ET), 0, stream, out, ln_out, x, y, bias, gamma, beta, rows, seq_len, vl, mode, eps, zero_ln_padded); break;
+      case 64: hipLaunchKernelGGL((tj::bias_residual_ln_small_kernel<16, TN>), sgrid, dim3(tj::ET), 0, stream, out, ln_out, x, y, bias, gamma, beta, rows, seq_len, vl, mode, eps, zero_ln_padded); break;
+      case 128: hipLaunchKernelGGL((tj::bias_residual_ln_small_kernel<32, TN>), sgrid, dim3(tj::ET), 0, stream, out, ln_out, x, y, bias, gamma, beta, rows, seq_len, vl, mode, eps, zero_ln_padded); break;
+      default: return TJ_ERR_UNSUPPORTED;
+    }
+    return tjh::launch_status();
+  }
   const dim3 grid((unsigned)((rows + tj::ET / 64 - 1) / (tj::ET / 64)));
   switch (cols / 256) {
     case 1: hipLaunchKernelGGL((tj::bias_residual_ln_kernel<1, TN>), grid, dim3(tj::ET), 0, stream, out, ln_out, x, y, bias, gamma, beta, rows, seq_len, vl, mode, eps, zero_ln_padded); break;
@@ -226,7 +290,7 @@ extern "C" int tj_bias_residual_layernorm(float* out, void* ln_out, int ln_dtype
   if (!tjh::product_below(tj::kMaxElements, {rows, cols})) return TJ_ERR_SHAPE;
   if (ln_dtype != TJ_F32 && ln_dtype != TJ_F16) return TJ_ERR_DTYPE;
   if ((mode != 0 || zero_ln_padded) && valid_len != nullptr && rows % seq_len != 0) return TJ_ERR_SHAPE;
-  if (cols % 256 != 0 || cols > 2048) return TJ_ERR_UNSUPPORTED;
+  if (!(cols == 32 || cols == 64 || cols == 128 || (cols % 256 == 0 && cols <= 2048))) return TJ_ERR_UNSUPPORTED;
   if (rows == 0) return TJ_OK;
   if (!ln_out || !x || !y || !bias || !gamma || !beta) return TJ_ERR_SHAPE;  // out may be null
   for (const void* p : {(const void*)out, (const void*)ln_out, (const void*)x, (const void*)y, (const void*)bias,

@@ -7,7 +7,7 @@ with one pass each; ``bias_residual_layernorm`` also produces the LayerNorm of
 the residual stream that the next step reads. ``bias_relu`` serves the
 optional post-norm / ReLU block. They return ``None`` for
 layouts the kernels do not take (non-fp32, a last dimension that is not a
-multiple of 4 -- of 256 up to 2048 for the norm --, unaligned or
+multiple of 4 -- one of ``NORM_WIDTHS`` for the norm --, unaligned or
 non-contiguous tensors), and the caller then uses the plain tensor ops.
 """
 
@@ -19,6 +19,9 @@ import torch
 
 from . import _lib
 from .attention import _stream_ptr
+
+#: Row widths the fused residual + LayerNorm kernel takes.
+NORM_WIDTHS = (32, 64, 128, 256, 512, 1024, 2048)
 
 MODE_PLAIN = 0       # out = x + y + b
 MODE_ZERO_Y = 1      # out = x + (row valid ? y + b : 0)
@@ -93,7 +96,7 @@ def bias_residual_layernorm(x: torch.Tensor, y: torch.Tensor, bias: torch.Tensor
     the shapes or the norm are not covered.
     """
     c = x.shape[-1] if x.ndim == 3 else 0
-    if (x.ndim != 3 or y.shape != x.shape or bias.shape != (c,) or c % 256 or c > 2048 or (c // 256) & (c // 256 - 1)
+    if (x.ndim != 3 or y.shape != x.shape or bias.shape != (c,) or c not in NORM_WIDTHS
             or not isinstance(norm, torch.nn.LayerNorm) or tuple(norm.normalized_shape) != (c,)
             or norm.weight is None or norm.bias is None):
         return None

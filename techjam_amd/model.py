@@ -19,6 +19,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .kernels.attention import scaled_dot_product_attention
+from .kernels.elementwise import NORM_WIDTHS
 
 
 ACTIVATIONS = ("gelu", "relu")
@@ -255,7 +256,7 @@ class EncoderBlock(nn.Module):
 
     def _post_norms_fusable(self, x) -> bool:
         c = x.shape[-1]
-        return (c in (256, 512, 1024, 2048)
+        return (c in NORM_WIDTHS
                 and all(type(n) is nn.LayerNorm and n.elementwise_affine and n.bias is not None
                         and n.weight.dtype == torch.float32 for n in (self.norm1, self.norm2)))
 
@@ -403,7 +404,7 @@ class TransformerEncoder(nn.Module):
         if not self.norm_first:
             return False
         norms = [m for layer in self.layers for m in (layer.norm1, layer.norm2)] + [self.final_norm]
-        return (len(self.layers) > 0 and d in (256, 512, 1024, 2048)
+        return (len(self.layers) > 0 and d in NORM_WIDTHS
                 and all(layer._can_fuse(x, valid_token_mask, valid_len) for layer in self.layers)
                 and all(type(n) is nn.LayerNorm and n.elementwise_affine and n.bias is not None
                         and n.weight.dtype == torch.float32 for n in norms))

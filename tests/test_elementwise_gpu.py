@@ -73,7 +73,7 @@ def test_unsupported_layouts_are_declined(cuda):
     assert bias_gelu(y.half(), bias.half()) is None                     # fp32 only
 
 
-@pytest.mark.parametrize("c", [256, 512, 1024, 2048])
+@pytest.mark.parametrize("c", [32, 64, 128, 256, 512, 1024, 2048])
 @pytest.mark.parametrize("masked", [False, True])
 def test_bias_residual_layernorm_matches_tensor_ops(cuda, c, masked):
     """The residual pass is bitwise the tensor ops; the fused LayerNorm is
@@ -108,7 +108,7 @@ def test_bias_residual_layernorm_in_place_and_unsupported_widths(cuda):
     out, ln = bias_residual_layernorm(x, y, bias, lens, MODE_ZERO_OUT, norm, out=y)
     assert out.data_ptr() == y.data_ptr() and torch.equal(out, want)
     assert (ln - F.layer_norm(want, (512,), norm.weight, norm.bias, norm.eps)).abs().max().item() < 2e-5
-    for c in (64, 768, 4096):  # not a power-of-two multiple of 256 up to 2048
+    for c in (16, 96, 768, 4096):  # none of 32, 64, 128 or a power-of-two multiple of 256 up to 2048
         x, y, bias, lens, _ = _case(cuda, c=c, seed=22)
         assert bias_residual_layernorm(x, y, bias, lens, MODE_ZERO_OUT, torch.nn.LayerNorm(c).to(cuda)) is None
 
