@@ -11,9 +11,9 @@
 //   S_quad[(i,j), v] += sum_t b_ti b_tj v_tv,  S_lin[j, v] += sum_t b_tj v_tv,
 //   G[i, j] += sum_t b_ti b_tj,  z[j] += sum_t b_tj,  S_const[v] += sum_t v_tv.
 //
-// Launches advance KG = 8 chunks at a time; in launch L every head owns 47
+// Launches advance KG = 8 chunks at a time; in launch L every head owns 31
 // workgroups with four roles:
-//   * apply (4 per chunk, 128 rows each, for the eight chunks whose start
+//   * apply (2 per chunk, 256 rows each, for the eight chunks whose start
 //     states the previous launch produced): quadratic term as
 //       y^T = sum_i S_i^T (a_i * a^T)  (S_i = rows (i, .) of S_quad),
 //     i.e. 64 MFMA GEMMs whose B operand is the fp16 product a_i*a_j built in
@@ -48,7 +48,7 @@ namespace {
 constexpr int PD = 64;         // head dim (d = dv)
 constexpr int PC = 512;        // chunk length
 constexpr int PT = 256;        // threads per workgroup
-constexpr int NAPPLY = 4;      // apply workgroups per head and chunk (128 rows each)
+constexpr int NAPPLY = 2;      // apply workgroups per head and chunk (256 rows each)
 constexpr int NUPD = 6;        // quad-update workgroups per head (4 for i < 32, 2 for i >= 32)
 constexpr int KG = 8;          // chunks per launch (update sub-chunks, apply groups)
 constexpr int NSLOT = 2 * KG;  // shadow slots: state_c lives in slot c % NSLOT
@@ -56,7 +56,6 @@ constexpr int NCONV = KG;      // token-image workgroups per head (one chunk eac
 constexpr int NROLE = KG * NAPPLY + NUPD + 1 + NCONV;
 constexpr int LP = 72;         // padded LDS row of 64 halves (144 bytes)
 constexpr int kBufferFlags = 0x00020000;  // raw (untyped) buffer resource word 3 on gfx950
-constexpr int AP = 66;         // padded LDS row of the a tile (132 bytes, conflict-free u16 reads)
 
 // Workspace of one head (byte offsets).
 constexpr size_t kQuadImg = 0;                                   // fp32 [64 i][2 jb][2 vb][64 lanes][16]
@@ -75,14 +74,13 @@ constexpr size_t kTokImgBytes = size_t(KG) * (PC / 64) * kTileImg;  // one launc
 constexpr size_t kTokImg = (kZsShadow + NSLOT * 128 * 4 + 255) & ~size_t(255);  // [2][kTokImgBytes]
 constexpr size_t kPerHead = kTokImg + 2 * kTokImgBytes;
 
-// LDS: apply = quad-state ring (49152) or diagonal tiles (36864), + a tile (16896);
+// LDS: apply = quad-state ring (49152) or diagonal tiles (36864);
 //      updates = two transposed token tiles, double buffered (36864).
 constexpr int kRing = 3;                        // quad-state stages in flight
 constexpr int kRingStage = 2 * PD * PD * 2;     // one stage: rows of two i, [2][64 v][64 j] fp16
 constexpr int kStageBytes = kRing * kRingStage;
 static_assert(kStageBytes >= 4 * 64 * LP * 2, "diagonal / update tiles must fit the ring area");
-constexpr int kATileBytes = 128 * AP * 2;
-constexpr int kSmemBytes = kStageBytes + kATileBytes;
+constexpr int kSmemBytes = kStageBytes;
 
 struct PolyArgs {
   const void* q;
@@ -207,41 +205,63 @@ __device__ __forceinline__ half8_t mul8(half8_t x, half_t s) {
 }
 
 // ---------------------------------------------------------------------------
-// Apply role: rows [row0, row0 + 128) of the chunk.
+// Apply role: rows [row0, row0 + 256) of the chunk; each wave owns RB = 2
+// blocks of 32 consecutive rows, so every state fragment read from LDS feeds
+// two MFMAs and every ring stage serves 256 rows.
 // ---------------------------------------------------------------------------
 template <typename T>
-__device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int m, int c, int qt, char* smem) {
+__device__ __forceinline__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int m, int c, int qt, char* smem) {
+  constexpr int RB = 2;
+  constexpr int WROWS = 32 * RB;
   const int t0 = c * PC, t1 = min(a.S, t0 + PC), slot = c % NSLOT;
-  const int row0 = t0 + 128 * qt;
-  if (row0 >= t1 || row0 + 128 <= a.prefix_end) return;
+  const int row0 = t0 + 4 * WROWS * qt;
+  if (row0 >= t1 || row0 + 4 * WROWS <= a.prefix_end) return;
   auto kb = reinterpret_cast<half_t(*)[64][LP]>(smem);                  // diag: [2][64][LP]
   auto vt = reinterpret_cast<half_t(*)[64][LP]>(smem + 2 * 64 * LP * 2);  // diag: [2][64][LP]
-  auto at = reinterpret_cast<half_t(*)[AP]>(smem + kStageBytes);       // [128][AP]
 
   const int tid = threadIdx.x, w = tid / kWave, lane = tid % kWave, hl = lane / 32, ln = lane % 32;
-  const int qw0 = row0 + 32 * w;
-  const int qi = qw0 + ln;
-  const int qrow = 32 * w + ln;
+  const int qw0 = row0 + WROWS * w;
 
   // a = fp16(q * rs); B operand slots (hl, j) <-> dim 16*ks + 8*hl + j.
-  half8_t aB[4];
+  half8_t aB[RB][4];
   {
     const T* qp = reinterpret_cast<const T*>(a.q);
-    const bool in = qi < t1;
-    const int64_t base = a.vq.row(b, h, in ? qi : t0);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      float x[8];
-      load_row4<T>(qp + base + 16 * ks + 8 * hl, x);
-      load_row4<T>(qp + base + 16 * ks + 8 * hl + 4, x + 4);
+    for (int rb = 0; rb < RB; ++rb) {
+      const int qi = qw0 + 32 * rb + ln;
+      const bool in = qi < t1;
+      const int64_t base = a.vq.row(b, h, in ? qi : t0);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) aB[ks][j] = in ? (half_t)(x[j] * a.rs) : (half_t)0.f;
-      // AP rows are only 4-byte aligned: store as four half2.
+      for (int ks = 0; ks < 4; ++ks) {
+        float x[8];
+        load_row4<T>(qp + base + 16 * ks + 8 * hl, x);
+        load_row4<T>(qp + base + 16 * ks + 8 * hl + 4, x + 4);
 #pragma unroll
-      for (int j = 0; j < 8; j += 2)
-        *reinterpret_cast<half2_t*>(&at[qrow][16 * ks + 8 * hl + j]) = half2_t{aB[ks][j], aB[ks][j + 1]};
+        for (int j = 0; j < 8; ++j) aB[rb][ks][j] = in ? (half_t)(x[j] * a.rs) : (half_t)0.f;
+      }
     }
   }
+  // Linear denominator a.z (z = S_lin's row sums, fp32 in the slot's small
+  // shadow), taken while few registers are live.
+  const float* zs = reinterpret_cast<const float*>(ws + kZsShadow) + slot * 128;
+  float den_l[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    float dl = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) dl += (float)aB[rb][ks][j] * zs[16 * ks + 8 * hl + j];
+    den_l[rb] = pair_sum(dl);
+  }
+  // a_i, a_i+1 (i = 2p) of this lane's query: dword p & 3 of aB[rb][p >> 3],
+  // held by the lane half (p >> 2) & 1; the lane-pair swap hands it to both.
+  auto a_pair = [&](int rb, int p) -> half2_t {
+    using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
+    const uint32_t u = __builtin_bit_cast(u32x4, aB[rb][p >> 3])[p & 3];
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __builtin_bit_cast(half2_t, ((p >> 2) & 1) ? r[1] : r[0]);
+  };
 
   const half_t* qshadow = reinterpret_cast<const half_t*>(ws + kQuadShadow) + size_t(slot) * PD * PD * PD;
   // The fp16 quad shadow of one i is piece-major, [8 q][64 v][8 j]: piece q
@@ -289,11 +309,15 @@ __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int 
     }
   };
 
-  float16_t accq[2];
+  // accq: the quadratic numerator first; after the ring, scaled by c2 and
+  // joined by c1 times the linear term and by the exact diagonal block.
+  float16_t accq[RB][2];
 #pragma unroll
-  for (int vb = 0; vb < 2; ++vb)
+  for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) accq[vb][r] = 0.f;
+    for (int vb = 0; vb < 2; ++vb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) accq[rb][vb][r] = 0.f;
 
   // One ring step: MFMAs on the pairs of stage sc, after issuing stage sc + 2.
   auto step = [&](auto sc) {
@@ -309,18 +333,23 @@ __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int 
 #pragma unroll
     for (int gp = 0; gp < G; ++gp) {
       const int p = p0 + gp;
+      half2_t ap[RB];
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) ap[rb] = a_pair(rb, p);
 #pragma unroll
       for (int ii = 0; ii < 2; ++ii) {
-        const half_t ai = at[qrow][2 * p + ii];
-        const half_t ai2 = ai + ai;
 #pragma unroll
         for (int ks = ib; ks < 4; ++ks) {
-          const half8_t bop = mul8(aB[ks], ks == ib ? ai : ai2);
           const int k = 2 * (gp * np + 2 * ks + hl - 2 * ib) + ii;
+          half8_t sa[2];
 #pragma unroll
-          for (int vb = 0; vb < 2; ++vb) {
-            const half8_t sa = *reinterpret_cast<const half8_t*>(base + k * 1024 + (32 * vb + ln) * 16);
-            accq[vb] = mfma32(sa, bop, accq[vb]);
+          for (int vb = 0; vb < 2; ++vb) sa[vb] = *reinterpret_cast<const half8_t*>(base + k * 1024 + (32 * vb + ln) * 16);
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb) {
+            const half_t ai = ap[rb][ii];
+            const half8_t bop = mul8(aB[rb][ks], ks == ib ? ai : (half_t)(ai + ai));
+#pragma unroll
+            for (int vb = 0; vb < 2; ++vb) accq[rb][vb] = mfma32(sa[vb], bop, accq[rb][vb]);
           }
         }
       }
@@ -338,55 +367,57 @@ __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int 
   };
   issue(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
   issue(std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
-  __builtin_amdgcn_s_waitcnt(0x0074);  // stage 0 landed (stage 1: four copies in flight); a tile stores done
+  __builtin_amdgcn_s_waitcnt(0x0074);  // stage 0 landed (stage 1: four copies in flight)
   lds_barrier();
   static_for<0, kSteps>(step);
 
   // Linear numerator term S_lin^T a^T and the quadratic denominator G a^T
-  // (operands straight from the L2-resident shadows).
+  // (operands straight from the L2-resident shadows). G's rows are read in
+  // the order that swaps bits 2 and 3 of the row index, so that accumulator
+  // element r of this lane holds row 32 blk + 16 (r / 8) + 8 hl + r % 8 --
+  // the dims this lane's own aB[rb][2 blk + r / 8][r % 8] holds -- and
+  // a^T G a needs no other lane's a.
+  const float c0 = a.coeffs[3 * m], c1 = a.coeffs[3 * m + 1], c2 = a.coeffs[3 * m + 2];
   const half_t* lsh = reinterpret_cast<const half_t*>(ws + kLinShadow) + size_t(slot) * PD * PD;
   const half_t* gsh = reinterpret_cast<const half_t*>(ws + kGramShadow) + size_t(slot) * PD * PD;
-  const float* zs = reinterpret_cast<const float*>(ws + kZsShadow) + slot * 128;
-  float16_t accl[2], ug[2];
+  const int grow = (ln & 0x13) | ((ln & 4) << 1) | ((ln & 8) >> 1);
+  float den_q[RB], den_d[RB];
 #pragma unroll
-  for (int blk = 0; blk < 2; ++blk)
+  for (int rb = 0; rb < RB; ++rb) den_q[rb] = den_d[rb] = 0.f;
+  // One 32-row block of S_lin^T (output block blk = v block) and of G at a time,
+  // each fragment feeding both query blocks.
 #pragma unroll
-    for (int r = 0; r < 16; ++r) accl[blk][r] = ug[blk][r] = 0.f;
+  for (int blk = 0; blk < 2; ++blk) {
+    half8_t la[4], ga[4];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
-      const half8_t la = *reinterpret_cast<const half8_t*>(lsh + (32 * blk + ln) * PD + 16 * ks + 8 * hl);
-      const half8_t ga = *reinterpret_cast<const half8_t*>(gsh + (32 * blk + ln) * PD + 16 * ks + 8 * hl);
-      accl[blk] = mfma32(la, aB[ks], accl[blk]);
-      ug[blk] = mfma32(ga, aB[ks], ug[blk]);
-    }
-  // a^T G a: rows i of ug pair with a_i from the a tile; a.z over this lane's 32 dims.
-  float den_q = 0.f, den_l = 0.f;
-#pragma unroll
-  for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int i = 32 * blk + 8 * (r / 4) + 4 * hl + (r % 4);
-      den_q += (float)at[qrow][i] * ug[blk][r];
+    for (int ks = 0; ks < 4; ++ks) {
+      la[ks] = *reinterpret_cast<const half8_t*>(lsh + (32 * blk + ln) * PD + 16 * ks + 8 * hl);
+      ga[ks] = *reinterpret_cast<const half8_t*>(gsh + (32 * blk + grow) * PD + 16 * ks + 8 * hl);
     }
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
+    for (int rb = 0; rb < RB; ++rb) {
+      float16_t tl, tg;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) den_l += (float)aB[ks][j] * zs[16 * ks + 8 * hl + j];
-  den_q = pair_sum(den_q);
-  den_l = pair_sum(den_l);
+      for (int r = 0; r < 16; ++r) tl[r] = tg[r] = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        tl = mfma32(la[ks], aB[rb][ks], tl);
+        tg = mfma32(ga[ks], aB[rb][ks], tg);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        den_q[rb] += (float)aB[rb][2 * blk + r / 8][r % 8] * tg[r];
+        accq[rb][blk][r] = c2 * accq[rb][blk][r] + c1 * tl[r];
+      }
+    }
+  }
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) den_q[rb] = pair_sum(den_q[rb]);
 
-  // Exact diagonal block: keys [t0, min(t1, row0 + 128)), no max subtraction.
-  float16_t accd[2];
-#pragma unroll
-  for (int vb = 0; vb < 2; ++vb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) accd[vb][r] = 0.f;
-  float den_d = 0.f;
-  const int key_end = min(t1, row0 + 128);
+  // Exact diagonal block: keys [t0, min(t1, row0 + 256)), no max subtraction;
+  // the weighted values accumulate straight into accq.
+  const int key_end = min(t1, row0 + 4 * WROWS);
   const int n_kt = (key_end - t0 + 63) / 64;
-  const int wave_last = min(qw0 + 31, key_end - 1);
   TokTile<T> tile;
   tile.init(a, b, h, tid);
   tile.load(t0);
@@ -396,63 +427,71 @@ __device__ void apply_role(const PolyArgs& a, const char* ws, int b, int h, int 
     const int cur = kt & 1;
     const int kv0 = t0 + 64 * kt;
     if (kt + 1 < n_kt) tile.load(kv0 + 64);
-    if (kv0 <= wave_last) {
-      float16_t s[2];
 #pragma unroll
-      for (int kh = 0; kh < 2; ++kh) {
+    for (int rb = 0; rb < RB; ++rb) {
+      const int qb0 = qw0 + 32 * rb;
+      const int qi = qb0 + ln;
+      // a block whose rows all precede the tile (or lie past the chunk) skips it
+      if (kv0 <= min(qb0 + 31, key_end - 1)) {
+        float16_t s[2];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[kh][r] = 0.f;
+        for (int kh = 0; kh < 2; ++kh) {
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const half8_t kf = *reinterpret_cast<const half8_t*>(&kb[cur][32 * kh + ln][16 * ks + 8 * hl]);
-          s[kh] = mfma32(kf, aB[ks], s[kh]);
+          for (int r = 0; r < 16; ++r) s[kh][r] = 0.f;
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) {
+            const half8_t kf = *reinterpret_cast<const half8_t*>(&kb[cur][32 * kh + ln][16 * ks + 8 * hl]);
+            s[kh] = mfma32(kf, aB[rb][ks], s[kh]);
+          }
         }
+        half8_t pf[4];
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = kv0 + 32 * kh + 8 * (r / 4) + 4 * hl + (r % 4);
+            const float wgt = key <= qi ? fast_exp2(s[kh][r] * 1.4426950408889634f) : 0.f;
+            const half_t wh = (half_t)wgt;
+            den_d[rb] += (float)wh;
+            pf[2 * kh + r / 8][r % 8] = wh;
+          }
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+          for (int vb = 0; vb < 2; ++vb) {
+            const half8_t vf = *reinterpret_cast<const half8_t*>(&vt[cur][32 * vb + ln][16 * st + 8 * hl]);
+            accq[rb][vb] = mfma32(vf, pf[st], accq[rb][vb]);
+          }
       }
-      half8_t pf[4];
-#pragma unroll
-      for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kv0 + 32 * kh + 8 * (r / 4) + 4 * hl + (r % 4);
-          const float wgt = key <= qi ? fast_exp2(s[kh][r] * 1.4426950408889634f) : 0.f;
-          const half_t wh = (half_t)wgt;
-          den_d += (float)wh;
-          pf[2 * kh + r / 8][r % 8] = wh;
-        }
-#pragma unroll
-      for (int st = 0; st < 4; ++st)
-#pragma unroll
-        for (int vb = 0; vb < 2; ++vb) {
-          const half8_t vf = *reinterpret_cast<const half8_t*>(&vt[cur][32 * vb + ln][16 * st + 8 * hl]);
-          accd[vb] = mfma32(vf, pf[st], accd[vb]);
-        }
     }
     if (kt + 1 < n_kt) tile.store_diag(kb[cur ^ 1], vt[cur ^ 1], a.rs, tid);
     __syncthreads();
   }
-  den_d = pair_sum(den_d);
 
-  if (qi >= t1 || qi < a.prefix_end) return;
-  const float c0 = a.coeffs[3 * m], c1 = a.coeffs[3 * m + 1], c2 = a.coeffs[3 * m + 2];
-  const float den = c0 * (float)t0 + c1 * den_l + c2 * den_q + den_d;
-  const float inv = 1.f / den;
-  T* op = reinterpret_cast<T*>(a.o) + a.vo.row(b, h, qi);
 #pragma unroll
-  for (int vb = 0; vb < 2; ++vb)
+  for (int rb = 0; rb < RB; ++rb) {
+    const int qi = qw0 + 32 * rb + ln;
+    const float dd = pair_sum(den_d[rb]);
+    if (qi >= t1 || qi < a.prefix_end) continue;
+    const float den = c0 * (float)t0 + c1 * den_l[rb] + c2 * den_q[rb] + dd;
+    const float inv = 1.f / den;
+    T* op = reinterpret_cast<T*>(a.o) + a.vo.row(b, h, qi);
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int v0 = 32 * vb + 8 * g + 4 * hl;
-      const float4_t sc = ld4(zs + 64 + v0);
-      float y[4];
+    for (int vb = 0; vb < 2; ++vb)
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        y[e] = (c0 * sc[e] + c1 * accl[vb][4 * g + e] + c2 * accq[vb][4 * g + e] + accd[vb][4 * g + e]) * inv;
-      if constexpr (sizeof(T) == 4) {
-        *reinterpret_cast<float4_t*>(op + v0) = float4_t{y[0], y[1], y[2], y[3]};
-      } else {
-        *reinterpret_cast<half4_t*>(op + v0) = half4_t{(half_t)y[0], (half_t)y[1], (half_t)y[2], (half_t)y[3]};
+      for (int g = 0; g < 4; ++g) {
+        const int v0 = 32 * vb + 8 * g + 4 * hl;
+        const float4_t sc = ld4(zs + 64 + v0);
+        float y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = (c0 * sc[e] + accq[rb][vb][4 * g + e]) * inv;
+        if constexpr (sizeof(T) == 4) {
+          *reinterpret_cast<float4_t*>(op + v0) = float4_t{y[0], y[1], y[2], y[3]};
+        } else {
+          *reinterpret_cast<half4_t*>(op + v0) = half4_t{(half_t)y[0], (half_t)y[1], (half_t)y[2], (half_t)y[3]};
+        }
       }
-    }
+  }
 }
 
 // ---------------------------------------------------------------------------

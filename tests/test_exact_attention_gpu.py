@@ -308,6 +308,31 @@ def test_random_configurations_match_brute_force(cuda, case):
     _assert_close(out.float(), ref, max_abs=4e-3 if not case["f16"] else 6e-3, what=str(case))
 
 
+@pytest.mark.parametrize("split", [False, True])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_rows_past_the_sequence_end_read_as_zeros(cuda, dtype, causal, split):
+    """K and V views whose memory continues past row S - 1 with NaN. S = 1000
+    is not a multiple of the 64-key tile, so the last tile reaches 24 rows
+    past the end; the bounds-checked buffer loads must return zeros there (a
+    NaN value row times a zero weight would still poison every output row)."""
+    from techjam_amd.kernels import scaled_dot_product_attention
+
+    b, h, s, d, pad = 2, 3, 1000, 64, 64
+    q, k, v = (_draw((b, h, s, d), seed, dtype=dtype) for seed in (11, 12, 13))
+    views = [q.to(cuda)]
+    for t in (k, v):
+        full = torch.full((b, h, s + pad, d), float("nan"), device=cuda, dtype=dtype)
+        full[:, :, :s] = t.to(cuda)
+        views.append(full[:, :, :s])
+    out = torch.full((b, h, s, d), float("nan"), device=cuda, dtype=dtype)
+    scaled_dot_product_attention(*views, is_causal=causal, out=out, qk_split=True if split else None)
+    torch.cuda.synchronize()
+    ref = brute_force_attention(q, k, v, d ** -0.5, causal)
+    _assert_close(out.float(), ref, max_abs=4e-3 if dtype == torch.float32 else 6e-3,
+                  what=f"{dtype} causal={causal} split={split}")
+
+
 @pytest.mark.parametrize("causal", [True, False])
 def test_wide_tiles_with_ragged_lengths(cuda, causal):
     """B=8 H=16 S=2048 takes the 256-row tile path (1024 wide tiles) with
