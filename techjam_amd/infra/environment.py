@@ -19,7 +19,18 @@ from pathlib import Path
 from typing import Any, Dict, List, Optional
 
 
+def under_profiler() -> bool:
+    """True inside a rocprofv3 run (it exports ROCPROF_* settings). Its
+    preloaded library follows every child process and, when counters are
+    collected, starts the GPU there before the child's own program runs; a
+    child that is a script (``rocm-smi`` starts through ``env python3``) would
+    then replace itself after that start. The probes run no tools then."""
+    return any(k.startswith("ROCPROF_") for k in os.environ)
+
+
 def _command_output(command: List[str], timeout: float = 10.0) -> Optional[str]:
+    if under_profiler():
+        return None
     try:
         done = subprocess.run(command, capture_output=True, text=True, timeout=timeout, check=False)
     except (OSError, subprocess.SubprocessError):

@@ -108,3 +108,23 @@ def test_bench_git_record_falls_back_to_the_library_build_record(monkeypatch, tm
     assert rec["commit"] == "abc123" and rec["library_sources_match"] is True
     info.write_text('{"commit": "abc123", "library_sources_dirty": false, "library_source_digest": "0"}')
     assert bench.git_record()["library_sources_match"] is False
+
+
+def test_environment_probes_start_no_tools_under_a_profiler(monkeypatch):
+    """Inside rocprofv3 (ROCPROF_* set) the git and rocm-smi probes run no
+    child process: the profiler's preload would start the GPU in the child
+    before a script there replaces itself."""
+    import subprocess
+
+    from techjam_amd.infra import environment as env
+
+    def refuse(*args, **kwargs):
+        raise AssertionError(f"a tool was started: {args}")
+
+    monkeypatch.setattr(subprocess, "run", refuse)
+    monkeypatch.setenv("ROCPROF_COUNTER_COLLECTION", "1")
+    assert env.under_profiler()
+    assert env.collect_gpu_state(torch.device("cuda", 0)) is None
+    assert env.collect_git()["commit"] is None
+    monkeypatch.delenv("ROCPROF_COUNTER_COLLECTION")
+    assert not env.under_profiler()
