@@ -74,6 +74,45 @@ def test_fused_scan_matches_oracle_scan(cuda, n, prefix):
     assert rel < 5e-3 and bad == 0
 
 
+def _scan_cases(n_cases, seed):
+    """Random shapes for the fused scan: lengths from one token to 24 chunks,
+    exact prefixes anywhere (also inside a chunk), fp32 and fp16 inputs."""
+    import random
+
+    rng = random.Random(seed)
+    cases = []
+    for i in range(n_cases):
+        n = rng.choice([rng.randint(1, 600), rng.randint(500, 5000), rng.randint(4000, 12000)])
+        cases.append(dict(seed=seed + i, b=rng.randint(1, 2), h=rng.randint(1, 3), n=n,
+                          prefix=rng.choice([0, 0, rng.randint(0, n - 1)]), f16=rng.random() < 0.3))
+    return cases
+
+
+@pytest.mark.parametrize("case", _scan_cases(16, 31), ids=lambda c: "b{b}h{h}n{n}p{prefix}{}".format("h" if c["f16"] else "", **c))
+def test_fused_scan_random_shapes(cuda, case):
+    from techjam_amd.kernels.poly import poly_rows
+
+    b, h, n, prefix = case["b"], case["h"], case["n"], case["prefix"]
+    g = torch.Generator().manual_seed(case["seed"])
+    q, k, v = (torch.randn(b, h, n, 64, generator=g) * 0.577 for _ in range(3))
+    dt = torch.float16 if case["f16"] else torch.float32
+    q, k, v = (t.to(dt).float() for t in (q, k, v))
+    coeffs = coefficient_table(torch.rand(b, h, generator=g) * 0.3 + 0.1)
+    ref = poly_linear_attention(q, k, v, 64 ** -0.5, chunk=512, exact_prefix=prefix, coeffs=coeffs,
+                                skip_final_state_update=True)
+    out = torch.full((b, h, n, 64), 777.0, device=cuda, dtype=dt)
+    poly_rows(q.to(cuda, dt), k.to(cuda, dt), v.to(cuda, dt), 64 ** -0.5, coeffs.float().reshape(-1, 3).to(cuda),
+              chunk=512, exact_prefix=prefix, out=out)
+    torch.cuda.synchronize()
+    got = out.float().cpu()
+    if prefix:
+        assert bool((got[:, :, :prefix] == 777.0).all()), "rows inside the exact prefix were written"
+    tail = slice(prefix, n)
+    bad, mx = _or_failures(got[:, :, tail], ref[:, :, tail])
+    rel = _rel_rms(got[:, :, tail], ref[:, :, tail])
+    assert bad == 0 and rel < 5e-3, f"{case}: rel_rms={rel:.2e} max_abs={mx:.2e} failed={bad}"
+
+
 def test_rows_past_the_sequence_end_read_as_zeros(cuda):
     """Token tiles of 64 reach past S = 1000 + 37: K and V views whose memory
     continues with NaN after row S - 1 must give the same output as compact
