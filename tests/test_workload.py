@@ -128,3 +128,26 @@ def test_environment_probes_start_no_tools_under_a_profiler(monkeypatch):
     assert env.collect_git()["commit"] is None
     monkeypatch.delenv("ROCPROF_COUNTER_COLLECTION")
     assert not env.under_profiler()
+
+
+@pytest.mark.parametrize("argv,env,message", [
+    (["--gpus", "2"], {}, "one GPU only"),
+    ([], {"WORLD_SIZE": "4"}, "one GPU only"),
+    ([], {"HIP_VISIBLE_DEVICES": ""}, "needs a ROCm GPU"),
+])
+def test_bench_refuses_what_it_does_not_measure(argv, env, message):
+    """The driver contract on a machine that cannot run it: more than one GPU
+    (flag or launcher environment) and no GPU both end with exit status 2 and
+    a message, before any device work."""
+    import os
+    import subprocess
+    import sys
+
+    if message == "needs a ROCm GPU" and torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    run_env = dict(os.environ, **env)
+    res = subprocess.run([sys.executable, str(ROOT / "bench.py"), *argv], capture_output=True, text=True,
+                         env=run_env, timeout=300)
+    assert res.returncode == 2, res.stderr[-2000:]
+    assert message in res.stderr
+    assert res.stdout.strip() == ""
