@@ -8,8 +8,9 @@
 // Work decomposition
 //   * One workgroup = 4 waves = a tile of 128 query rows of one (b, h); each
 //     wave owns 32 consecutive rows for the whole key loop.
-//   * Keys stream through LDS in tiles of 64 (double buffered): K row-major,
-//     V transposed, both converted to fp16 while being stored.
+//   * Keys stream through LDS in tiles of 64 (32 for the split-score kernel
+//     with two query blocks per wave) -- double buffered: K row-major, V
+//     transposed, both converted to fp16 while being stored.
 //   * Scores are computed transposed, S^T = K Q^T (keys x queries), so a lane
 //     holds 32 keys of ONE query: the row max/sum is lane-local plus one swap
 //     with lane ^ 32, the rescale factor is a per-lane scalar, and the fp32
@@ -42,7 +43,7 @@
 namespace tj {
 namespace {
 
-constexpr int BN = 64;     // keys per tile
+constexpr int BN = 64;     // keys per tile (kernels take a tile width BNT: 64, or 32)
 constexpr int NT = 256;    // threads per workgroup
 constexpr int PAD = 8;     // fp16 padding per LDS row (16 bytes)
 constexpr float kRescaleLog2 = 8.f;  // lazy-rescale threshold of the running max (log2 units)
@@ -78,34 +79,36 @@ struct Tile {
   static_assert(NC % 4 == 0, "head_dim too small for the load mapping");
 };
 
-template <int HD>
+template <int HD, int BNT>
 struct SmemBase {
-  half_t k[2][BN][HD + PAD];   // K tile (high part), row-major
-  half_t vt[2][HD][BN + PAD];  // V tile, transposed, columns in key_slot order
+  half_t k[2][BNT][HD + PAD];   // K tile (high part), row-major
+  half_t vt[2][HD][BNT + PAD];  // V tile, transposed, columns in key_slot order
 };
 
 // Kernels that may meet split heads also carry the low part of K.
-template <int HD, bool SPLIT_OK>
-struct Smem : SmemBase<HD> {};
+template <int HD, bool SPLIT_OK, int BNT>
+struct Smem : SmemBase<HD, BNT> {};
 
-template <int HD>
-struct Smem<HD, true> : SmemBase<HD> {
-  half_t klo[2][BN][HD + PAD];
+template <int HD, int BNT>
+struct Smem<HD, true, BNT> : SmemBase<HD, BNT> {
+  half_t klo[2][BNT][HD + PAD];
 };
 
-// Global -> register staging of one key tile. Unit u covers keys 4g .. 4g+3 of
-// the tile and one 16-byte column vector c; lanes 4n .. 4n+3 share g so a
-// 16-lane LDS store phase touches 4 rows x 4 columns.
+// Global -> register staging of one key tile of 16 KPU keys. Unit u covers
+// keys KPU g .. KPU g + KPU - 1 of the tile (KPU = 4, or 2 for 32-key tiles)
+// and one 16-byte column vector c; lanes 4n .. 4n+3 share g so a 16-lane LDS
+// store phase touches KPU rows x 4 columns.
 //
 // K and V are read with bounds-checked buffer loads: one resource per (b, h)
 // spans rows 0 .. S-1 (byte offsets fit 31 bits, checked on the host), so
 // keys at or past S read as zeros without a branch, and the per-tile address
 // arithmetic is scalar: lane offset (4g, c) + scalar offset (kv0 + r) * stride.
-template <typename T, int HD>
+template <typename T, int HD, int KPU>
 struct KVStage {
   using TL = Tile<T, HD>;
-  Vec16<T> kx[TL::UPT][4];
-  Vec16<T> vx[TL::UPT][4];
+  static_assert(KPU == 4 || (KPU == 2 && sizeof(T) == 4), "two-key units for fp32 inputs only");
+  Vec16<T> kx[TL::UPT][KPU];
+  Vec16<T> vx[TL::UPT][KPU];
   __amdgpu_buffer_rsrc_t rk, rv;
   uint32_t koff[TL::UPT], voff[TL::UPT];
   uint32_t kstep, vstep;  // bytes per key row
@@ -128,8 +131,8 @@ struct KVStage {
     for (int p = 0; p < TL::UPT; ++p) {
       int g, c;
       unit_coords(tid + p * NT, g, c);
-      koff[p] = 4 * g * kstep + c * TL::VEC * (uint32_t)sizeof(T);
-      voff[p] = 4 * g * vstep + c * TL::VEC * (uint32_t)sizeof(T);
+      koff[p] = KPU * g * kstep + c * TL::VEC * (uint32_t)sizeof(T);
+      voff[p] = KPU * g * vstep + c * TL::VEC * (uint32_t)sizeof(T);
     }
   }
 
@@ -138,7 +141,7 @@ struct KVStage {
     for (int p = 0; p < TL::UPT; ++p) {
       if (tid + p * NT < TL::UNITS) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
+        for (int r = 0; r < KPU; ++r) {
           kx[p][r].v = __builtin_bit_cast(decltype(kx[p][r].v),
                                           __builtin_amdgcn_raw_buffer_load_b128(rk, koff[p], (kv0 + r) * kstep, 0));
           vx[p][r].v = __builtin_bit_cast(decltype(vx[p][r].v),
@@ -157,7 +160,7 @@ struct KVStage {
         int g, c;
         unit_coords(u, g, c);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
+        for (int r = 0; r < KPU; ++r) {
 #pragma unroll
           for (int e = 0; e < TL::VEC; e += 4) {
             half4_t hk, lk;
@@ -167,12 +170,18 @@ struct KVStage {
               hk[j] = (half_t)x;
               lk[j] = (half_t)(x - (float)hk[j]);
             }
-            *reinterpret_cast<half4_t*>(&sm.k[buf][4 * g + r][c * TL::VEC + e]) = hk;
-            if constexpr (SPLIT) *reinterpret_cast<half4_t*>(&sm.klo[buf][4 * g + r][c * TL::VEC + e]) = lk;
+            *reinterpret_cast<half4_t*>(&sm.k[buf][KPU * g + r][c * TL::VEC + e]) = hk;
+            if constexpr (SPLIT) *reinterpret_cast<half4_t*>(&sm.klo[buf][KPU * g + r][c * TL::VEC + e]) = lk;
           }
         }
-        const int slot = key_slot(4 * g);
-        if constexpr (sizeof(T) == 2) {
+        const int slot = key_slot(KPU * g);
+        if constexpr (KPU == 2) {
+#pragma unroll
+          for (int e = 0; e < TL::VEC; ++e) {
+            half2_t hv = {(half_t)vx[p][0].get(e), (half_t)vx[p][1].get(e)};
+            *reinterpret_cast<half2_t*>(&sm.vt[buf][c * TL::VEC + e][slot]) = hv;
+          }
+        } else if constexpr (sizeof(T) == 2) {
           // fp16 rows: dword m of the four key rows holds elements 2m, 2m+1;
           // byte permutes gather them column-wise (element-wise extraction
           // from a 16-byte register goes through scratch memory).
@@ -204,10 +213,12 @@ struct KVStage {
 // One query tile of one (b, h): 4 waves x 32*QB rows. Each wave holds QB
 // 32-row query blocks, so every K / V^T operand read from LDS feeds QB MFMAs.
 // SPLIT selects the three-MFMA score path.
-template <typename T, int HD, int QB, bool SPLIT, typename SM>
+template <typename T, int HD, int QB, bool SPLIT, int BNT, typename SM>
 __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int h, int q0, int row_cap,
                                           int L) {
   using TL = Tile<T, HD>;
+  constexpr int NKB = BNT / 32;  // 32-key score blocks per tile
+  constexpr int NS = BNT / 16;   // 16-key PV steps per tile
   constexpr int WROWS = 32 * QB;
   constexpr int TROWS = 4 * WROWS;
   const int tid = threadIdx.x;
@@ -221,7 +232,7 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
   // by the epilogue); a tile with none of them streams no keys at all.
   const int row_end = min(min(q0 + TROWS, L), row_cap);
   const int kv_end = q0 >= row_end ? 0 : (a.causal ? row_end : L);
-  const int n_kv = kv_end > 0 ? (kv_end + BN - 1) / BN : 0;
+  const int n_kv = kv_end > 0 ? (kv_end + BNT - 1) / BNT : 0;
   // Last key this wave needs (inclusive); waves whose rows are all padding
   // (or beyond row_cap) compute nothing.
   int wave_last_key = a.causal ? min(qw0 + WROWS - 1, kv_end - 1) : kv_end - 1;
@@ -284,7 +295,7 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
       for (int r = 0; r < 16; ++r) oacc[qb][db][r] = 0.f;
   }
 
-  KVStage<T, HD> stage;
+  KVStage<T, HD, BNT / 16> stage;
   stage.init(a, b, h, tid);
   if (n_kv > 0) {
     stage.load(0, tid);
@@ -294,16 +305,16 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
 
   for (int kt = 0; kt < n_kv; ++kt) {
     const int cur = kt & 1;
-    const int kv0 = kt * BN;
-    if (kt + 1 < n_kv) stage.load(kv0 + BN, tid);
+    const int kv0 = kt * BNT;
+    if (kt + 1 < n_kv) stage.load(kv0 + BNT, tid);
 
     if (kv0 <= wave_last_key) {
       // Scores come out of the MFMA already shifted by the running max: the
       // accumulator starts at -m_run (0 on the first tile, where m_run is set).
       const bool first = kv0 == 0;
-      float16_t sacc[QB][2];
+      float16_t sacc[QB][NKB];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
         for (int ks = 0; ks < TL::KS; ++ks) {
           const half8_t kf = *reinterpret_cast<const half8_t*>(&sm.k[cur][kb * 32 + ln][16 * ks + 8 * hl]);
@@ -322,18 +333,18 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
           }
         }
 
-      half8_t pf[QB][4];
+      half8_t pf[QB][NS];
       float shift[QB];
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
         const int qb0 = qw0 + 32 * qb;
         const int qi = qb0 + ln;
         // Mask keys past the diagonal (causal) or past the valid length.
-        const bool need_mask = a.causal ? (kv0 + BN - 1 > qb0) : (kv0 + BN > L);
+        const bool need_mask = a.causal ? (kv0 + BNT - 1 > qb0) : (kv0 + BNT > L);
         if (need_mask) {
           const int lim = a.causal ? qi : L - 1;
 #pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
+          for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
               const int key = kv0 + kb * 32 + 8 * (r / 4) + 4 * hl + (r % 4);
@@ -342,7 +353,7 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
         }
         float t_max = sacc[qb][0][0];
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
           for (int r = 0; r < 16; ++r) t_max = fmaxf(t_max, sacc[qb][kb][r]);
         t_max = pair_max(t_max);
@@ -367,7 +378,7 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
 #pragma unroll
             for (int r = 0; r < 16; ++r) oacc[qb][db][r] *= alpha;
 #pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
+          for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) sacc[qb][kb][r] -= shift[qb];
 #pragma unroll
@@ -379,12 +390,12 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
         // P = exp2(S) rounded to fp16; the row sum adds the same rounded
         // values (a dominant key's rounding then cancels in the normalisation).
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
+        for (int s = 0; s < NS; ++s)
 #pragma unroll
           for (int j = 0; j < 8; ++j) pf[qb][s][j] = (half_t)fast_exp2(sacc[qb][s / 2][8 * (s % 2) + j]);
         float psum = 0.f;
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
+        for (int s = 0; s < NS; ++s)
 #pragma unroll
           for (int j = 0; j < 8; j += 2)
             psum = __builtin_amdgcn_fdot2(half2_t{pf[qb][s][j], pf[qb][s][j + 1]},
@@ -393,7 +404,7 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
       }
       // O^T += V^T P^T over four 16-key steps.
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
+      for (int s = 0; s < NS; ++s)
 #pragma unroll
         for (int db = 0; db < TL::DB; ++db) {
           const half8_t vf = *reinterpret_cast<const half8_t*>(&sm.vt[cur][db * 32 + ln][16 * s + 8 * hl]);
@@ -436,9 +447,9 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
   }
 }
 
-template <typename T, int HD, int QB, bool SPLIT_OK>
+template <typename T, int HD, int QB, bool SPLIT_OK, int BNT = BN>
 __global__ __launch_bounds__(NT, (HD > 128 ? 1 : 2)) void attn_fwd_kernel(AttnArgs a) {
-  __shared__ Smem<HD, SPLIT_OK> sm;
+  __shared__ Smem<HD, SPLIT_OK, BNT> sm;
 
   // XCD-aware tile order: ids x, x+8, x+16, ... run on XCD x.
   const int id = blockIdx.x;
@@ -494,14 +505,14 @@ __global__ __launch_bounds__(NT, (HD > 128 ? 1 : 2)) void attn_fwd_kernel(AttnAr
 
   if constexpr (SPLIT_OK) {
     if (a.qk_split[bh] != 0) {
-      attn_tile<T, HD, QB, true>(a, sm, b, h, q0, row_cap, L);
+      attn_tile<T, HD, QB, true, BNT>(a, sm, b, h, q0, row_cap, L);
       return;
     }
   }
-  attn_tile<T, HD, QB, false>(a, sm, b, h, q0, row_cap, L);
+  attn_tile<T, HD, QB, false, BNT>(a, sm, b, h, q0, row_cap, L);
 }
 
-template <typename T, int HD, int QB>
+template <typename T, int HD, int QB, int BNT = BN>
 int launch_qb(AttnArgs a, hipStream_t stream) {
   a.n_mtiles = (a.S + 128 * QB - 1) / (128 * QB);
   const int64_t bhn = int64_t(a.B) * a.H;
@@ -511,26 +522,32 @@ int launch_qb(AttnArgs a, hipStream_t stream) {
   const int64_t per_xcd = (bhn + kNumXcd - 1) / kNumXcd;
   const int64_t grid = a.balanced ? bhn * a.n_mtiles : kNumXcd * (per_xcd + a.group - 1) * a.n_mtiles;
   if (grid * NT >= (int64_t(1) << 32)) return TJ_ERR_SHAPE;
-  if constexpr (QB == 1 && HD <= 128) {
+  if constexpr ((QB == 1 && HD <= 128) || BNT == 32) {
     if (a.qk_split != nullptr) {
-      hipLaunchKernelGGL((attn_fwd_kernel<T, HD, QB, true>), dim3(uint32_t(grid)), dim3(NT), 0, stream, a);
+      hipLaunchKernelGGL((attn_fwd_kernel<T, HD, QB, true, BNT>), dim3(uint32_t(grid)), dim3(NT), 0, stream, a);
       return tjh::launch_status();
     }
   }
-  hipLaunchKernelGGL((attn_fwd_kernel<T, HD, QB, false>), dim3(uint32_t(grid)), dim3(NT), 0, stream, a);
+  hipLaunchKernelGGL((attn_fwd_kernel<T, HD, QB, false, BNT>), dim3(uint32_t(grid)), dim3(NT), 0, stream, a);
   return tjh::launch_status();
 }
 
-// Two query blocks per wave halve LDS operand traffic per MFMA. They fit the
-// register budget only for head_dim <= 64 without split scores, and need
-// sequences long enough to fill 256-row tiles. Launches with fewer than 1024
-// such tiles (two per CU) keep 128-row tiles: there the heaviest tile sets
-// the time, and a 32-row block per wave halves its per-key-tile work.
+// Two query blocks per wave halve LDS operand traffic and staging per MFMA.
+// They fit the register budget for head_dim <= 64 (with split scores only at
+// head_dim 64 with 32-key tiles, fp32 inputs), and need sequences long enough
+// to fill 256-row tiles. Launches with fewer than 1024 such tiles (two per CU)
+// keep 128-row tiles: there the heaviest tile sets the time, and a 32-row
+// block per wave halves its per-key-tile work.
 template <typename T, int HD>
 int launch(const AttnArgs& a, hipStream_t stream) {
   if constexpr (HD <= 64) {
     const int64_t wide_tiles = int64_t(a.B) * a.H * ((a.S + 255) / 256);
-    if (a.S >= 512 && a.qk_split == nullptr && wide_tiles >= 1024) return launch_qb<T, HD, 2>(a, stream);
+    if (a.S >= 512 && wide_tiles >= 1024) {
+      if (a.qk_split == nullptr) return launch_qb<T, HD, 2>(a, stream);
+      // Split scores carry K's low half and Q's as well: two query blocks
+      // per wave fit only with 32-key tiles (fp32 inputs, head_dim 64).
+      if constexpr (HD == 64 && sizeof(T) == 4) return launch_qb<T, HD, 2, 32>(a, stream);
+    }
   }
   return launch_qb<T, HD, 1>(a, stream);
 }

@@ -359,6 +359,50 @@ def test_wide_tiles_with_ragged_lengths(cuda, causal):
         assert torch.count_nonzero(out[bi, :, n:]).item() == 0
 
 
+@pytest.mark.parametrize("mode", ["causal", "padded", "row_limits"])
+def test_split_scores_on_wide_tiles(cuda, mode):
+    """Split scores for every head on a grid of 1024 256-row tiles (B=8 H=16
+    S=2048): the kernel with two query blocks per wave and 32-key tiles.
+    Scores have sd ~4 (q, k ~ N(0, 2^2)), the range split scores exist for;
+    every (b, h) against the blockwise oracle on the GPU in fp32. `padded`
+    adds right padding without causality; `row_limits` computes only the
+    first rows of some heads (the guarded route's launch) and must leave the
+    others' rows untouched."""
+    from techjam_amd.kernels import scaled_dot_product_attention
+
+    b, s, h, d = 8, 2048, 16, 64
+    g = torch.Generator(device=cuda).manual_seed(78)
+    q, k = (torch.randn(b, s, h, d, generator=g, device=cuda).transpose(1, 2) * 2.0 for _ in range(2))
+    v = torch.randn(b, s, h, d, generator=g, device=cuda).transpose(1, 2)
+    causal = mode != "padded"
+    lengths = (torch.tensor([2048, 1, 0, 257, 1024, 2047, 700, 1500], dtype=torch.int32, device=cuda)
+               if mode == "padded" else None)
+    limits = None
+    if mode == "row_limits":
+        limits = torch.full((b * h,), s, dtype=torch.int32, device=cuda)
+        limits[1::3] = 300
+        limits[2::5] = 0
+    out = torch.full((b, s, h, d), float("nan"), device=cuda).transpose(1, 2)
+    scaled_dot_product_attention(q, k, v, is_causal=causal, valid_len=lengths, out=out,
+                                 qk_split=torch.ones(b * h, dtype=torch.int32, device=cuda),
+                                 row_limit=limits)
+    torch.cuda.synchronize()
+    prev = torch.get_float32_matmul_precision()
+    torch.set_float32_matmul_precision("highest")
+    try:
+        ref = blockwise_attention(q, k, v, d ** -0.5, causal, valid_len=lengths, block_q=512, block_k=512)
+    finally:
+        torch.set_float32_matmul_precision(prev)
+    rows = torch.ones(b, h, s, dtype=torch.bool, device=cuda)
+    if limits is not None:
+        rows = torch.arange(s, device=cuda)[None, None, :] < limits.view(b, h, 1)
+        assert bool(torch.isnan(out[~rows]).all()), "rows beyond a row limit were written"
+    err = (out - ref).abs()[rows]
+    ok = torch.isfinite(out[rows]) & ((err <= ATOL) | (err <= RTOL * ref[rows].abs()))
+    assert int((~ok).sum()) == 0, f"{int((~ok).sum())} failing, max abs {float(err.max()):.3e}"
+    assert float(err.max()) < 4e-3, f"max abs {float(err.max()):.3e}"
+
+
 def test_keys_spanning_more_than_2_gib_are_copied_not_refused(cuda):
     """k and v rows 4 MiB apart (600 rows span 2.3 GiB, beyond the kernels'
     31-bit offsets): the wrapper reads them through a contiguous copy, and the
