@@ -6,8 +6,9 @@
 // src/implementations/extreme.py:227-236, poly_reference.py:262-264).
 //
 // Work decomposition
-//   * One workgroup = 4 waves = a tile of 128 query rows of one (b, h); each
-//     wave owns 32 consecutive rows for the whole key loop.
+//   * One workgroup = 4 waves = a tile of 128 QB query rows of one (b, h);
+//     each wave owns QB blocks of 32 consecutive rows (QB = 1 or 2) for the
+//     whole key loop.
 //   * Keys stream through LDS in tiles of 64 (32 for the split-score kernel
 //     with two query blocks per wave) -- double buffered: K row-major, V
 //     transposed, both converted to fp16 while being stored.
@@ -102,7 +103,7 @@ struct Smem<HD, true, BNT> : SmemBase<HD, BNT> {
 // K and V are read with bounds-checked buffer loads: one resource per (b, h)
 // spans rows 0 .. S-1 (byte offsets fit 31 bits, checked on the host), so
 // keys at or past S read as zeros without a branch, and the per-tile address
-// arithmetic is scalar: lane offset (4g, c) + scalar offset (kv0 + r) * stride.
+// arithmetic is scalar: lane offset (KPU g, c) + scalar offset (kv0 + r) * stride.
 template <typename T, int HD, int KPU>
 struct KVStage {
   using TL = Tile<T, HD>;
