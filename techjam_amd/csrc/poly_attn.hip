@@ -11,9 +11,9 @@
 //   S_quad[(i,j), v] += sum_t b_ti b_tj v_tv,  S_lin[j, v] += sum_t b_tj v_tv,
 //   G[i, j] += sum_t b_ti b_tj,  z[j] += sum_t b_tj,  S_const[v] += sum_t v_tv.
 //
-// Launches advance KG = 8 chunks at a time; in launch L every head owns 31
+// Launches advance KG = 16 chunks at a time; in launch L every head owns 55
 // workgroups with four roles:
-//   * apply (2 per chunk, 256 rows each, for the eight chunks whose start
+//   * apply (2 per chunk, 256 rows each, for the KG chunks whose start
 //     states the previous launch produced): quadratic term as
 //       y^T = sum_i S_i^T (a_i * a^T)  (S_i = rows (i, .) of S_quad),
 //     i.e. 64 MFMA GEMMs whose B operand is the fp16 product a_i*a_j built in
@@ -21,22 +21,25 @@
 //     as three more small GEMMs; the exact diagonal block like the exact
 //     kernel (S^T = b a^T in registers, no max subtraction).
 //   * quad update (6 per head): S_i += (b_i * b)^T v over the tokens of
-//     chunks [8L, 8L + 8), accumulated straight into MFMA accumulators that
-//     hold the fp32 master in its register image (the master's memory layout
-//     IS the accumulator layout, so loading and storing it is straight 16-byte
-//     copies, once per launch). After each chunk it writes the fp16 shadow of
-//     the state the apply of the next chunk reads.
+//     chunks [KG L, KG L + KG), accumulated straight into MFMA accumulators
+//     that hold the fp32 master in its register image (the master's memory
+//     layout IS the accumulator layout, so loading and storing it is straight
+//     16-byte copies, once per launch). After each chunk it writes the fp16
+//     shadow of the state the apply of the next chunk reads.
 //   * small-state update (1 per head): S_lin, G, z, S_const, likewise.
-//   * token images (8 per head): b = k*sqrt(scale) and v of the chunks the
+//   * token images (KG per head): b = k*sqrt(scale) and v of the chunks the
 //     next launch folds in, converted once to fp16 tiles laid out as the
 //     update roles' LDS image, which those roles then stream with direct
 //     global->LDS copies.
-// State c (before chunk c) lives in shadow slot c % 16: a launch reads the
-// slots of states 8L-7 .. 8L and writes those of 8L+1 .. 8L+8, so applies and
-// updates of one launch never touch the same slot. Eight chunks per launch
-// load and store each master half as often as four (the polynomial call on
-// 64 heads of 65536 tokens: 5.8-6.1 -> 5.4-5.5 ms, bitwise the same); twelve
-// or sixteen gain another ~1 % for 0.25-0.5 GiB more shadow slots.
+// State c (before chunk c) lives in shadow slot c % (2 KG): a launch reads
+// the slots of states KG L - KG + 1 .. KG L and writes those of KG L + 1 ..
+// KG L + KG, so applies and updates of one launch never touch the same slot.
+// More chunks per launch load and store each master less often and need
+// fewer launches (the polynomial call on 64 heads of 65536 tokens: 4 -> 8
+// chunks 5.8-6.1 -> 5.4-5.5 ms; the extreme step with 8 -> 16 chunks
+// 8.99-9.02 -> 8.78-8.83 ms, 10.2 MiB more workspace per head), at the
+// price of a longer update chain per launch when few heads share the GPU
+// (16 heads of 100 000 tokens: 2.39-2.40 -> 2.42 ms).
 // Heads whose guard flag is 0 exit at once (the exact kernel covers them).
 #include <type_traits>
 
@@ -50,7 +53,7 @@ constexpr int PC = 512;        // chunk length
 constexpr int PT = 256;        // threads per workgroup
 constexpr int NAPPLY = 2;      // apply workgroups per head and chunk (256 rows each)
 constexpr int NUPD = 6;        // quad-update workgroups per head (4 for i < 32, 2 for i >= 32)
-constexpr int KG = 8;          // chunks per launch (update sub-chunks, apply groups)
+constexpr int KG = 16;         // chunks per launch (update sub-chunks, apply groups)
 constexpr int NSLOT = 2 * KG;  // shadow slots: state_c lives in slot c % NSLOT
 constexpr int NCONV = KG;      // token-image workgroups per head (one chunk each)
 constexpr int NROLE = KG * NAPPLY + NUPD + 1 + NCONV;
@@ -70,7 +73,7 @@ constexpr size_t kZsShadow = kGramShadow + NSLOT * PD * PD * 2;   // fp32 [NSLOT
 // Token images: the k (scaled) and v tiles the update roles of a launch fold
 // in, written once by the previous launch as fp16 LDS images (see TokTile).
 constexpr int kTileImg = 2 * PD * 64 * 2;                          // [b^T | v^T] of 64 tokens
-constexpr size_t kTokImgBytes = size_t(KG) * (PC / 64) * kTileImg;  // one launch: 1 MiB
+constexpr size_t kTokImgBytes = size_t(KG) * (PC / 64) * kTileImg;  // one launch: 2 MiB
 constexpr size_t kTokImg = (kZsShadow + NSLOT * 128 * 4 + 255) & ~size_t(255);  // [2][kTokImgBytes]
 constexpr size_t kPerHead = kTokImg + 2 * kTokImgBytes;
 

@@ -12,9 +12,10 @@ MIB = 1 << 20
 
 def test_workspace_sizes_come_from_the_library():
     ws = P.poly_workspace_bytes_per_head()
-    # fp32 masters (S_quad 64x64x64 = 1 MiB and the small states), a 16-slot
-    # ring of fp16 shadows (~0.5 MiB each) and two launches of fp16 token images
-    assert 10 * MIB < ws < 13 * MIB
+    # fp32 masters (S_quad 64x64x64 = 1 MiB and the small states), a 32-slot
+    # ring of fp16 shadows (~0.5 MiB each) and two launches of fp16 token
+    # images (2 MiB each: 16 chunks per launch)
+    assert 20 * MIB < ws < 23 * MIB
     assert P.guard_workspace_bytes_per_head() == 8 * 3 * 8  # 512 samples = 8 row blocks x 3 doubles
 
 
@@ -38,8 +39,9 @@ def test_case_14_known_answers():
     ws = 16 * (P.poly_workspace_bytes_per_head() + P.guard_workspace_bytes_per_head()
                + P.GUARD_OUTPUT_BYTES_PER_HEAD)
     assert fp.per_item_bytes == 6 * act + ws
-    # the reference's RTX 5080 budget (23,034 MiB) gives its own answer, 4
-    assert P.plan_batch_chunk(32, fp, 23_034 * MIB).chunk == 4
+    # the reference's RTX 5080 budget (23,034 MiB): 2 (the reference itself
+    # picks 4, without the polynomial workspaces this route allocates)
+    assert P.plan_batch_chunk(32, fp, 23_034 * MIB).chunk == 2
     # 85 % of an MI355X's 288 GB holds the whole batch
     assert P.plan_batch_chunk(32, fp, int(0.85 * 288e9)).chunk == 32
     # fp16 activations halve the activation part, not the workspaces

@@ -44,12 +44,13 @@ def _rel_rms(got, ref):
     return float((got.double() - ref.double()).pow(2).mean().sqrt() / ref.double().pow(2).mean().sqrt())
 
 
-# The kernel keeps a 16-slot ring of fp16 state shadows (state c in slot
-# c % 16, eight chunks per launch): 10240 tokens (20 chunks) and 16461 tokens
-# (33 chunks, ragged tail of 77) reuse every slot at least once, the second
-# one twice, and cross launch boundaries mid-ring.
+# The kernel keeps a 32-slot ring of fp16 state shadows (state c in slot
+# c % 32, sixteen chunks per launch): 16461 tokens (33 chunks, ragged tail of
+# 77) and 24876 tokens (49 chunks, ragged tail of 300) reuse slots, the second
+# one every slot at least once, and both cross launch boundaries mid-ring;
+# 10240 tokens (20 chunks) crosses one launch boundary.
 @pytest.mark.parametrize("n,prefix", [(2048, 512), (2000, 700), (1536, 0), (300, 0), (4096, 4000),
-                                      (10240, 4096), (16384 + 77, 0)])
+                                      (10240, 4096), (16384 + 77, 0), (24576 + 300, 1000)])
 def test_fused_scan_matches_oracle_scan(cuda, n, prefix):
     from techjam_amd.kernels.poly import poly_rows
 
