@@ -95,6 +95,19 @@ struct Smem<HD, true, BNT> : SmemBase<HD, BNT> {
   half_t klo[2][BNT][HD + PAD];
 };
 
+// Low fp16 parts of x0, x1 given their packed fp16 roundings h: fp16(x - h),
+// one v_fma_mix per element (x * 1 - h in fp32, rounded once to fp16). x - h
+// is exact in fp32, so this is the rounded fp32 difference bit for bit, in one
+// instruction instead of a convert back to fp32, a subtract and a convert.
+__device__ __forceinline__ uint32_t low_parts(float x0, float x1, uint32_t h) {
+  uint32_t lo;
+  asm("v_fma_mixlo_f16 %0, %1, 1.0, -%3 op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mixhi_f16 %0, %2, 1.0, -%3 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
+      : "=&v"(lo)
+      : "v"(x0), "v"(x1), "v"(h));
+  return lo;
+}
+
 // Global -> register staging of one key tile of 16 KPU keys. Unit u covers
 // keys KPU g .. KPU g + KPU - 1 of the tile (KPU = 4, or 2 for 32-key tiles)
 // and one 16-byte column vector c; lanes 4n .. 4n+3 share g so a 16-lane LDS
@@ -164,15 +177,17 @@ struct KVStage {
         for (int r = 0; r < KPU; ++r) {
 #pragma unroll
           for (int e = 0; e < TL::VEC; e += 4) {
-            half4_t hk, lk;
+            half4_t hk;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const float x = kx[p][r].get(e + j);
-              hk[j] = (half_t)x;
-              lk[j] = (half_t)(x - (float)hk[j]);
-            }
+            for (int j = 0; j < 4; ++j) hk[j] = (half_t)kx[p][r].get(e + j);
             *reinterpret_cast<half4_t*>(&sm.k[buf][KPU * g + r][c * TL::VEC + e]) = hk;
-            if constexpr (SPLIT) *reinterpret_cast<half4_t*>(&sm.klo[buf][KPU * g + r][c * TL::VEC + e]) = lk;
+            if constexpr (SPLIT) {
+              using u32x2 = uint32_t __attribute__((ext_vector_type(2)));
+              const u32x2 hw = __builtin_bit_cast(u32x2, hk);
+              const u32x2 lw = {low_parts(kx[p][r].get(e), kx[p][r].get(e + 1), hw[0]),
+                                low_parts(kx[p][r].get(e + 2), kx[p][r].get(e + 3), hw[1])};
+              *reinterpret_cast<half4_t*>(&sm.klo[buf][KPU * g + r][c * TL::VEC + e]) = __builtin_bit_cast(half4_t, lw);
+            }
           }
         }
         const int slot = key_slot(KPU * g);
