@@ -203,15 +203,26 @@ def scaled_dot_product_attention(
     return out
 
 
+#: Entries kept by each of the small device-tensor caches below (oldest
+#: dropped first), so that callers cycling through many shapes do not grow
+#: them without bound.
+CACHE_ENTRIES = 64
+
 _ONES: dict = {}
+
+
+def _cache_put(cache: dict, key, value):
+    if len(cache) >= CACHE_ENTRIES:
+        cache.pop(next(iter(cache)))
+    cache[key] = value
+    return value
 
 
 def _all_heads(n: int, dev: torch.device) -> torch.Tensor:
     key = (n, str(dev))
     t = _ONES.get(key)
     if t is None:
-        t = torch.ones(n, dtype=torch.int32, device=dev)
-        _ONES[key] = t
+        t = _cache_put(_ONES, key, torch.ones(n, dtype=torch.int32, device=dev))
     return t
 
 
@@ -242,8 +253,7 @@ def sample_index(n: int, samples: int, seed: int, device: torch.device) -> torch
     if idx is None:
         gen = torch.Generator().manual_seed(seed)
         cpu = torch.randperm(n, generator=gen)[: min(samples, n)].to(torch.int32)
-        idx = cpu.to(device)
-        _SAMPLE_CACHE[key] = idx
+        idx = _cache_put(_SAMPLE_CACHE, key, cpu.to(device))
     return idx
 
 

@@ -113,8 +113,8 @@ def quad_update(
         raise ValueError("the master state must be float32")
     if shadow is not None and (tuple(shadow.shape) != tuple(out.shape) or shadow.dtype != torch.float16):
         raise ValueError(f"shadow must be float16 shaped {tuple(out.shape)}, got {shadow.dtype} {tuple(shadow.shape)}")
-    if shadow is not None:
-        _require_device(shadow)
+    if shadow is not None and shadow.device != dev:
+        raise ValueError(f"shadow is on {shadow.device}, the other tensors on {dev}")
     _check_dims(d, vw)
     b16 = _pad_last(b, _W, torch.float16)
     v16 = _pad_last(v, _W, torch.float16)

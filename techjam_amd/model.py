@@ -112,7 +112,11 @@ def fp16_weight(owner: nn.Module, key: str, weight: torch.Tensor) -> torch.Tenso
     """Rounded fp16 copy of ``weight``, cached on ``owner`` and rebuilt
     whenever the weight is replaced or modified in place."""
     cache = owner.__dict__.setdefault("_fp16_weights", {})
-    tag = (weight.data_ptr(), weight._version, weight.device, tuple(weight.shape))
+    try:
+        version = weight._version
+    except RuntimeError:  # inference tensors carry no version counter
+        version = None
+    tag = (weight.data_ptr(), version, weight.device, tuple(weight.shape))
     hit = cache.get(key)
     if hit is None or hit[0] != tag:
         hit = (tag, weight.detach().to(torch.float16))

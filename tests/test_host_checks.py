@@ -79,3 +79,19 @@ def test_head_span_rule_for_keys():
     assert _head_span_bytes(bshd) >= MAX_HEAD_SPAN_BYTES
     assert _head_span_bytes(bshd.contiguous()) == s * d * 4 < MAX_HEAD_SPAN_BYTES
     assert _head_span_bytes(torch.empty((1, 1, 0, 64), device="meta")) == 0
+
+
+def test_device_tensor_caches_stay_bounded():
+    """The guard's row-sample cache keeps at most CACHE_ENTRIES entries, newest kept."""
+    from techjam_amd.kernels import attention as A
+
+    A._SAMPLE_CACHE.clear()
+    cpu = torch.device("cpu")
+    for n in range(600, 600 + A.CACHE_ENTRIES + 10):
+        idx = A.sample_index(n, 512, 0, cpu)
+        assert idx.numel() == 512 and int(idx.max()) < n
+    assert len(A._SAMPLE_CACHE) == A.CACHE_ENTRIES
+    last = (600 + A.CACHE_ENTRIES + 9, 512, 0, str(cpu))
+    assert last in A._SAMPLE_CACHE
+    assert A.sample_index(*last[:3], cpu) is A._SAMPLE_CACHE[last]
+    A._SAMPLE_CACHE.clear()

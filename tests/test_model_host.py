@@ -23,6 +23,15 @@ def test_fp16_weight_cache_follows_the_weight():
     assert fp16_weight(lin, "other", lin.bias).shape == (4,)          # keys are separate entries
 
 
+def test_fp16_weight_cache_takes_inference_tensors():
+    """Weights created under inference mode have no version counter."""
+    with torch.inference_mode():
+        lin = torch.nn.Linear(8, 4)
+        w16 = fp16_weight(lin, "weight", lin.weight)
+        assert torch.equal(w16, lin.weight.detach().half())
+        assert fp16_weight(lin, "weight", lin.weight) is w16
+
+
 def test_project_keeps_fp32_inputs_on_the_fp32_gemm():
     lin = torch.nn.Linear(8, 4, bias=False)
     x = torch.randn(2, 3, 8)
