@@ -19,6 +19,18 @@ def test_workspace_sizes_come_from_the_library():
     assert P.guard_workspace_bytes_per_head() == 8 * 3 * 8  # 512 samples = 8 row blocks x 3 doubles
 
 
+def test_poly_workspace_is_per_head_and_independent_of_length():
+    """The planner multiplies one head's workspace by the head count: the
+    library's size must not depend on the sequence length and must scale
+    with B*H."""
+    from techjam_amd.kernels.poly import workspace_bytes
+
+    per_head = P.poly_workspace_bytes_per_head()
+    for s in (512, 4097, 65536, 100_000):
+        assert workspace_bytes(1, 1, s, 64, 512) == per_head
+    assert workspace_bytes(4, 16, 65536, 64, 512) == 64 * per_head
+
+
 def test_case_6_known_answers():
     """Case 6: B=10000, S=128, d_model=128, H=4, FFN=128."""
     fp = P.encoder_item_footprint(128, 128, 4, 128)
