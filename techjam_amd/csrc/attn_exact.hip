@@ -38,7 +38,10 @@
 //   * Heads flagged in qk_split compute QK^T from a two-term fp16 expansion of
 //     q and k (x = hi + lo, both fp16) with three MFMAs -- hi.hi + hi.lo +
 //     lo.hi -- which restores fp32-level score accuracy where the score range
-//     is wide enough for fp16 rounding of q and k to show in the softmax.
+//     is wide enough for fp16 rounding of q and k to show in the softmax, and
+//     feed PV the probabilities as two fp16 parts as well (P = hi + lo, two
+//     MFMAs per step), so that the only rounding left on those heads is v's
+//     to fp16: an output moves by at most 2^-11 * sum_j p_j |v_j| / l.
 #include "tj_common.h"
 
 namespace tj {
@@ -283,7 +286,13 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
           if (in) x.load(qp + base + d0 + e); else x.zero();
 #pragma unroll
           for (int j = 0; j < Vec16<T>::N; ++j) {
-            const float y = (x.get(j) + bq[e + j]) * a.qscale;
+            float y = (x.get(j) + bq[e + j]) * a.qscale;
+            // Split heads: hi and lo must both come from this one rounded
+            // fp32 y. Left free, the compiler forms the lo part's hi from the
+            // exact product (one v_fma_mix rounding to fp16) and the MFMA
+            // operand from the rounded y; where y rounds onto an fp16
+            // midpoint the two differ by an fp16 ulp and hi + lo misses q.
+            if constexpr (SPLIT) asm("" : "+v"(y));
             const half_t hi = (half_t)y;
             qf[qb][ks][e + j] = hi;
             if constexpr (SPLIT) qlo[qb][ks][e + j] = (half_t)(y - (float)hi);
@@ -350,6 +359,7 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
         }
 
       half8_t pf[QB][NS];
+      half8_t pl[QB][SPLIT ? NS : 1];  // split heads: p - fp16(p), rounded to fp16
       float shift[QB];
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
@@ -403,29 +413,54 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
       }
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
-        // P = exp2(S) rounded to fp16; the row sum adds the same rounded
-        // values (a dominant key's rounding then cancels in the normalisation).
+        if constexpr (SPLIT) {
+          // Split heads: P = hi + lo, both fp16 (lo = fp16(p - hi)), so the PV
+          // MFMAs multiply p to about 2^-22 of its value; the row sum adds p
+          // itself in fp32, consistent with that.
+          float psum = 0.f;
 #pragma unroll
-        for (int s = 0; s < NS; ++s)
+          for (int s = 0; s < NS; ++s)
 #pragma unroll
-          for (int j = 0; j < 8; ++j) pf[qb][s][j] = (half_t)fast_exp2(sacc[qb][s / 2][8 * (s % 2) + j]);
-        float psum = 0.f;
+            for (int j = 0; j < 8; j += 2) {
+              const float p0 = fast_exp2(sacc[qb][s / 2][8 * (s % 2) + j]);
+              const float p1 = fast_exp2(sacc[qb][s / 2][8 * (s % 2) + j + 1]);
+              const half2_t hi = {(half_t)p0, (half_t)p1};
+              const half2_t lo = __builtin_bit_cast(half2_t, low_parts(p0, p1, __builtin_bit_cast(uint32_t, hi)));
+              pf[qb][s][j] = hi[0];
+              pf[qb][s][j + 1] = hi[1];
+              pl[qb][s][j] = lo[0];
+              pl[qb][s][j + 1] = lo[1];
+              psum += p0 + p1;
+            }
+          l_run[qb] += psum;
+        } else {
+          // P = exp2(S) rounded to fp16; the row sum adds the same rounded
+          // values (a dominant key's rounding then cancels in the normalisation).
 #pragma unroll
-        for (int s = 0; s < NS; ++s)
+          for (int s = 0; s < NS; ++s)
 #pragma unroll
-          for (int j = 0; j < 8; j += 2)
-            psum = __builtin_amdgcn_fdot2(half2_t{pf[qb][s][j], pf[qb][s][j + 1]},
-                                          half2_t{(half_t)1.f, (half_t)1.f}, psum, false);
-        l_run[qb] += psum;
+            for (int j = 0; j < 8; ++j) pf[qb][s][j] = (half_t)fast_exp2(sacc[qb][s / 2][8 * (s % 2) + j]);
+          float psum = 0.f;
+#pragma unroll
+          for (int s = 0; s < NS; ++s)
+#pragma unroll
+            for (int j = 0; j < 8; j += 2)
+              psum = __builtin_amdgcn_fdot2(half2_t{pf[qb][s][j], pf[qb][s][j + 1]},
+                                            half2_t{(half_t)1.f, (half_t)1.f}, psum, false);
+          l_run[qb] += psum;
+        }
       }
-      // O^T += V^T P^T over four 16-key steps.
+      // O^T += V^T P^T over 16-key steps (split heads: V^T (P_hi + P_lo)^T).
 #pragma unroll
       for (int s = 0; s < NS; ++s)
 #pragma unroll
         for (int db = 0; db < TL::DB; ++db) {
           const half8_t vf = *reinterpret_cast<const half8_t*>(&sm.vt[cur][db * 32 + ln][16 * s + 8 * hl]);
 #pragma unroll
-          for (int qb = 0; qb < QB; ++qb) oacc[qb][db] = mfma32(vf, pf[qb][s], oacc[qb][db]);
+          for (int qb = 0; qb < QB; ++qb) {
+            oacc[qb][db] = mfma32(vf, pf[qb][s], oacc[qb][db]);
+            if constexpr (SPLIT) oacc[qb][db] = mfma32(vf, pl[qb][s], oacc[qb][db]);
+          }
         }
     }
 

@@ -2,10 +2,10 @@
 
 Mirrors ``src/implementations/extreme.py:18-319``:
 
-* ``choose_batch_chunk_size`` / ``estimate_batch_chunk_size`` (``:40-117``):
-  largest power-of-two batch chunk whose working set fits a fraction of HBM.
-  The HIP kernels never materialise scores, so the dispatcher calls them with
-  ``score_copies=0``; the parameter stays for the reference's callers.
+* The reference's batch-chunk estimator (``:40-117``: a power-of-two chunk
+  from SDPA score-copy counts) has no counterpart here: chunk sizes come from
+  ``planner.plan_batch_chunk``, which budgets the HIP kernels' real working
+  set (they never materialise scores).
 * ``right_padded_lengths`` (``:120-133``), ``forward_batch_chunks`` with OOM
   halving (``:136-164``) and ``forward_prefix_chunks`` with trimmed equal-length
   groups (``:167-204``).
@@ -33,56 +33,11 @@ from .sdpa import StridedSDPASelfAttention
 
 CASE_6_CONFIG = (10000, 128, 128, 4, 128, True, 4)
 CASE_14_CONFIG = (32, 100000, 1024, 16, 1024, True, 2)
-DEFAULT_MEMORY_FRACTION = 0.85
 
 ChunkForward = Callable[[torch.Tensor, Optional[torch.Tensor]], torch.Tensor]
 
 # One switch returns the guarded modules to exact attention on every head.
 POLY_ATTENTION_ENABLED = True
-
-
-def choose_batch_chunk_size(x: torch.Tensor, num_heads: int, *, score_copies: int, activation_copies: int,
-                            memory_fraction: float = DEFAULT_MEMORY_FRACTION) -> int:
-    """Largest power-of-two batch chunk inside a conservative device-memory budget."""
-    if not 0.0 < memory_fraction <= 1.0:
-        raise ValueError("memory_fraction must be in (0, 1]")
-    if num_heads <= 0:
-        raise ValueError("num_heads must be positive")
-    if score_copies < 0 or activation_copies <= 0:
-        raise ValueError("memory-copy estimates must be non-negative")
-    if x.shape[0] <= 1 or x.device.type != "cuda":
-        return 1
-    free_bytes, total_bytes = torch.cuda.mem_get_info(x.device)
-    allocated = torch.cuda.memory_allocated(x.device)
-    reusable = max(0, torch.cuda.memory_reserved(x.device) - allocated)
-    headroom = max(0, int(total_bytes * memory_fraction) - allocated)
-    return estimate_batch_chunk_size(
-        batch_size=x.shape[0], seq_len=x.shape[1], d_model=x.shape[2], num_heads=num_heads,
-        element_size=x.element_size(), free_bytes=min(headroom, free_bytes + reusable),
-        total_bytes=total_bytes, score_copies=score_copies, activation_copies=activation_copies,
-        memory_fraction=memory_fraction,
-    )
-
-
-def estimate_batch_chunk_size(*, batch_size: int, seq_len: int, d_model: int, num_heads: int,
-                              element_size: int, free_bytes: int, total_bytes: int, score_copies: int,
-                              activation_copies: int,
-                              memory_fraction: float = DEFAULT_MEMORY_FRACTION) -> int:
-    """Power-of-two chunk from sizes: per item ``act*S*D*e + scores*S^2*H*e`` after reserving the output."""
-    if min(batch_size, seq_len, d_model, num_heads, element_size) <= 0:
-        raise ValueError("tensor dimensions and element_size must be positive")
-    if min(free_bytes, total_bytes) < 0:
-        raise ValueError("memory byte counts must be non-negative")
-    if not 0.0 < memory_fraction <= 1.0:
-        raise ValueError("memory_fraction must be in (0, 1]")
-    if score_copies < 0 or activation_copies <= 0:
-        raise ValueError("memory-copy estimates must be non-negative")
-    allowed = min(free_bytes, int(total_bytes * memory_fraction))
-    working = max(0, allowed - batch_size * seq_len * d_model * element_size)
-    per_item = (activation_copies * seq_len * d_model * element_size
-                + score_copies * seq_len * seq_len * num_heads * element_size)
-    n = max(1, min(batch_size, working // per_item))
-    return 1 << (int(n).bit_length() - 1)
 
 
 def right_padded_lengths(valid_token_mask: torch.Tensor) -> list:

@@ -75,23 +75,9 @@ def config_key(config) -> tuple:
             config.ffn_dim, config.causal, config.num_layers)
 
 
-#: Float32 GEMMs of at most this many multiply-adds run on rocBLAS: below it
-#: hipBLASLt's kernels sit at a ~19 us floor on this stack (256x256x256:
-#: 26 us, rocBLAS 8 us, and exact fp32); above ~2^30 hipBLASLt's fast mode
-#: wins (8192x512x1536: 51 us, rocBLAS 100 us).
-SMALL_GEMM_MACS = 1 << 29
-
-
 def _linear_f32(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """``F.linear`` on float32, with small GEMMs routed to rocBLAS."""
-    if (x.is_cuda and x.dtype == torch.float32
-            and (x.numel() // max(1, x.shape[-1])) * weight.shape[0] * weight.shape[1] <= SMALL_GEMM_MACS):
-        prev = torch.backends.cuda.preferred_blas_library()
-        torch.backends.cuda.preferred_blas_library("cublas")  # the rocBLAS backend on ROCm
-        try:
-            return F.linear(x, weight, bias)
-        finally:
-            torch.backends.cuda.preferred_blas_library(prev)
+    """``F.linear`` on torch's configured BLAS backend (no process-global
+    state is changed per call)."""
     return F.linear(x, weight, bias)
 
 

@@ -270,17 +270,6 @@ def test_prefix_chunks_trim_padding_and_restore_shape():
     assert calls == [((2, 4, 2), None), ((1, 2, 2), None), ((1, 1, 2), None)]
 
 
-def test_chunk_estimates_known_answers():
-    from techjam_amd.implementations.extreme import estimate_batch_chunk_size
-
-    assert estimate_batch_chunk_size(batch_size=10000, seq_len=128, d_model=128, num_heads=4, element_size=4,
-                                     free_bytes=24 * 2**30, total_bytes=24 * 2**30, score_copies=12,
-                                     activation_copies=12) == 4096
-    assert estimate_batch_chunk_size(batch_size=32, seq_len=100000, d_model=1024, num_heads=16, element_size=2,
-                                     free_bytes=23_034 * 2**20, total_bytes=23_034 * 2**20, score_copies=0,
-                                     activation_copies=12) == 4
-
-
 def test_guarded_module_route_predicate():
     from techjam_amd.implementations import extreme
 
