@@ -258,7 +258,8 @@ __device__ __forceinline__ void apply_role(const PolyArgs& a, const char* ws, in
     den_l[rb] = pair_sum(dl);
   }
   // a_i, a_i+1 (i = 2p) of this lane's query: dword p & 3 of aB[rb][p >> 3],
-  // held by the lane half (p >> 2) & 1; the lane-pair swap hands it to both.
+  // held by the lane half (p >> 2) & 1; the lane-pair swap hands it to both
+  // (r[0] from the lower-half lane, r[1] from the upper, as in pair_values).
   auto a_pair = [&](int rb, int p) -> half2_t {
     using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
     const uint32_t u = __builtin_bit_cast(u32x4, aB[rb][p >> 3])[p & 3];

@@ -60,10 +60,12 @@ __device__ __forceinline__ void static_for(F&& f) {
 }
 
 // Reductions over the lane pair (l, l ^ 32) through v_permlane32_swap, a VALU
-// op on gfx950, instead of an LDS permute. With both operands equal the swap
-// returns x[l] and x[l ^ 32] in its two results (which one lands where
-// depends on the half of the wave); max and sum do not care, and both lanes of
-// a pair get bitwise identical results.
+// op on gfx950, instead of an LDS permute. With both operands equal to x, the
+// swap gives every lane l the pair's two values in a fixed order: r[0] is x of
+// lane l & 31 (the lower half of the wave) and r[1] is x of lane (l & 31) + 32
+// (the upper half), in both lanes of the pair. So a lane can pick its partner's
+// value, or the value of a given half, by index (poly_attn.hip's a_pair relies
+// on this); max and sum give both lanes bitwise identical results.
 __device__ __forceinline__ void pair_values(float x, float& a, float& b) {
   const unsigned u = __float_as_uint(x);
   const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);

@@ -360,7 +360,14 @@ class DispatchingTransformer(TransformerEncoder):
             raise UnsupportedCaseError("case 14 chunks require float16 or float32 GPU input")
         if valid_token_mask is not None:
             raise ValueError("trim padding before the case 14 chunk")
-        return self.forward_layers(x, None, None, gemm_operands=self.case14_gemm_operands)
+        # A trimmed group of two or more samples (x[start:end, :n]) is a
+        # strided view; the fused layer stack reads contiguous rows.
+        x = x.contiguous()
+        # fp16 GEMM operands are the fused fp32-interface path; fp16 input
+        # (an fp16 model, the reference's _forward_sdpa branch for case 14)
+        # runs the layer loop in its own dtype.
+        operands = self.case14_gemm_operands if x.dtype == torch.float32 else "fp32"
+        return self.forward_layers(x, None, None, gemm_operands=operands)
 
     def _forward_case_14(self, x, valid_token_mask=None):
         chunk = self._plan_chunk(x, poly=True)

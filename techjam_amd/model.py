@@ -97,11 +97,13 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor]) 
 def fp16_weight(owner: nn.Module, key: str, weight: torch.Tensor) -> torch.Tensor:
     """Rounded fp16 copy of ``weight``, cached on ``owner`` and rebuilt
     whenever the weight is replaced or modified in place."""
-    cache = owner.__dict__.setdefault("_fp16_weights", {})
     try:
         version = weight._version
-    except RuntimeError:  # inference tensors carry no version counter
-        version = None
+    except RuntimeError:
+        # An inference tensor carries no version counter, so an in-place
+        # refill could not be seen: convert on every call instead of caching.
+        return weight.detach().to(torch.float16)
+    cache = owner.__dict__.setdefault("_fp16_weights", {})
     tag = (weight.data_ptr(), version, weight.device, tuple(weight.shape))
     hit = cache.get(key)
     if hit is None or hit[0] != tag:

@@ -108,3 +108,45 @@ def test_prefix_chunked_batch_with_padding_matches_linear_memory_oracle(cuda, ca
     print(f"case 14 prefix chunks (8192, 5000, 0): max_abs={res.max_abs_error:.3e} "
           f"failed={res.failed_elements}/{res.total_elements}")
     assert res.passed, f"{res.failed_elements} failing elements, max_abs {res.max_abs_error:.3e}"
+
+
+def test_prefix_group_of_equal_lengths_is_served(cuda, case14_models):
+    """Two padded samples of the same valid length form one prefix group,
+    whose trimmed slice x[0:2, :5000] is a strided view: the route copies it
+    to contiguous rows for the fused layer stack instead of refusing it."""
+    oracle, cand = case14_models
+    x, mask = _input(3, 8192, [5000, 5000, 8192], 1236)
+    x, mask = x.to(cuda), mask.to(cuda)
+    with torch.inference_mode(), _fp32_matmuls():
+        got = cand._forward_case_14(x, mask)
+        ref = oracle(x, mask)
+        torch.cuda.synchronize()
+    assert bool((got[:2, 5000:] == 0).all())
+    res = compare_outputs_streamed(ref, got)
+    print(f"case 14 prefix chunks (5000, 5000, 8192): max_abs={res.max_abs_error:.3e} "
+          f"failed={res.failed_elements}/{res.total_elements}")
+    assert res.passed, f"{res.failed_elements} failing elements, max_abs {res.max_abs_error:.3e}"
+
+
+def test_fp16_input_runs_the_fp16_model(cuda, case14_models):
+    """Case 14 also declares float16 input (an fp16 model, as the harness
+    builds it for that dtype; the reference routes it through its SDPA
+    module in fp16). The route serves it on the layer loop in fp16 -- fp16
+    operands, fp32 accumulation inside the GEMMs and the attention kernels --
+    and the result stays within the OR rule of the FP32 oracle."""
+    import copy
+
+    oracle, cand = case14_models
+    half = copy.deepcopy(cand).half()
+    x, mask = _input(2, 8192, [8192, 6000], 1237)
+    x, mask = x.to(cuda), mask.to(cuda)
+    with torch.inference_mode(), _fp32_matmuls():
+        got = half._forward_case_14(x.half(), mask)
+        ref = oracle(x.half().float(), mask)
+        torch.cuda.synchronize()
+    assert got.dtype == torch.float16
+    assert bool((got[1, 6000:] == 0).all())
+    res = compare_outputs_streamed(ref, got.float())
+    print(f"case 14 fp16 model, (8192, 6000): max_abs={res.max_abs_error:.3e} "
+          f"failed={res.failed_elements}/{res.total_elements}")
+    assert res.passed, f"{res.failed_elements} failing elements, max_abs {res.max_abs_error:.3e}"

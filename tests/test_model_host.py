@@ -23,13 +23,17 @@ def test_fp16_weight_cache_follows_the_weight():
     assert fp16_weight(lin, "other", lin.bias).shape == (4,)          # keys are separate entries
 
 
-def test_fp16_weight_cache_takes_inference_tensors():
-    """Weights created under inference mode have no version counter."""
+def test_fp16_weight_of_an_inference_tensor_follows_an_in_place_refill():
+    """Weights created under inference mode have no version counter, so an
+    in-place refill (same storage) cannot be detected: such weights are
+    converted on every call, never served from a stale cache."""
     with torch.inference_mode():
         lin = torch.nn.Linear(8, 4)
         w16 = fp16_weight(lin, "weight", lin.weight)
         assert torch.equal(w16, lin.weight.detach().half())
-        assert fp16_weight(lin, "weight", lin.weight) is w16
+        lin.weight.data.copy_(torch.full((4, 8), 3.0))          # same data_ptr
+        assert torch.equal(fp16_weight(lin, "weight", lin.weight), torch.full((4, 8), 3.0, dtype=torch.float16))
+    assert "_fp16_weights" not in lin.__dict__
 
 
 def test_project_keeps_fp32_inputs_on_the_fp32_gemm():
