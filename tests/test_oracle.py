@@ -228,3 +228,67 @@ def test_linear_memory_oracle_rejects_non_prefix_masks_and_fp16():
 
 def test_flops_constant_for_the_attention_core_workload():
     assert math.isclose(exact_attention_flops([4096] * 64, 16, 64), 2.19956e12, rel_tol=1e-5)
+
+
+def _torch_encoder_with_oracle_weights(model, cfg):
+    """``torch.nn.TransformerEncoder`` with pre-norm layers, exact GELU and a
+    final LayerNorm, carrying ``model``'s weights (q/k/v stacked into the
+    packed in-projection)."""
+    layer = torch.nn.TransformerEncoderLayer(cfg.d_model, cfg.num_heads, dim_feedforward=cfg.ffn_dim, dropout=0.0,
+                                             activation="gelu", batch_first=True, norm_first=True)
+    enc = torch.nn.TransformerEncoder(layer, cfg.num_layers, norm=torch.nn.LayerNorm(cfg.d_model),
+                                      enable_nested_tensor=False).double().eval()
+    with torch.no_grad():
+        for mine, theirs in zip(model.layers, enc.layers):
+            a = mine.attention
+            theirs.self_attn.in_proj_weight.copy_(torch.cat([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight]))
+            theirs.self_attn.in_proj_bias.copy_(torch.cat([a.q_proj.bias, a.k_proj.bias, a.v_proj.bias]))
+            theirs.self_attn.out_proj.weight.copy_(a.out_proj.weight)
+            theirs.self_attn.out_proj.bias.copy_(a.out_proj.bias)
+            theirs.linear1.load_state_dict(mine.ffn_in.state_dict())
+            theirs.linear2.load_state_dict(mine.ffn_out.state_dict())
+            theirs.norm1.load_state_dict(mine.norm1.state_dict())
+            theirs.norm2.load_state_dict(mine.norm2.state_dict())
+        enc.norm.load_state_dict(model.final_norm.state_dict())
+    return enc
+
+
+@pytest.mark.parametrize("layers", [1, 3])
+def test_dense_model_block_wiring_matches_torch_transformer_encoder(layers):
+    """The oracle's block wiring against a library routine, not a second
+    restatement: torch's pre-norm encoder (norm_first, exact GELU, no dropout,
+    final LayerNorm) with the same weights, causal mask, fp64. A slip in norm
+    placement, residual order, activation or the final norm moves outputs by
+    O(0.1); what remains here (~5e-8) is the reference's fp32 softmax
+    (``torch_transformer_benchmark.py:111``), kept in the oracle's fp64 mode."""
+    cfg = TransformerConfig(batch_size=2, seq_len=48, d_model=64, num_heads=4, ffn_dim=96, num_layers=layers,
+                            causal=True)
+    torch.manual_seed(3)
+    model = DenseTransformer(cfg).double().eval()
+    enc = _torch_encoder_with_oracle_weights(model, cfg)
+    x = torch.randn(2, 48, 64, dtype=torch.float64)
+    causal = torch.nn.Transformer.generate_square_subsequent_mask(48, dtype=torch.float64)
+    with torch.no_grad():
+        ref = enc(x, mask=causal, is_causal=True)
+        got = model(x)
+    assert torch.allclose(got, ref, atol=1e-6, rtol=0), float((got - ref).abs().max())
+
+
+def test_dense_model_padding_matches_torch_encoder_on_valid_rows():
+    """With right padding the oracle zeroes padded rows after every block
+    (reference ``torch_transformer_benchmark.py:120-121``, ``:145``, ``:170-171``);
+    under a causal mask those rows never reach a valid one, so the valid rows
+    equal torch's encoder with a key-padding mask, and the padded rows are 0."""
+    cfg = TransformerConfig(batch_size=3, seq_len=40, d_model=64, num_heads=4, ffn_dim=96, num_layers=2, causal=True)
+    torch.manual_seed(4)
+    model = DenseTransformer(cfg).double().eval()
+    enc = _torch_encoder_with_oracle_weights(model, cfg)
+    lengths = torch.tensor([40, 17, 1])
+    mask = torch.arange(40)[None, :] < lengths[:, None]
+    x = torch.randn(3, 40, 64, dtype=torch.float64).masked_fill(~mask[..., None], 0)
+    causal = torch.nn.Transformer.generate_square_subsequent_mask(40, dtype=torch.float64)
+    with torch.no_grad():
+        ref = enc(x, mask=causal, src_key_padding_mask=~mask, is_causal=True)
+        got = model(x, mask)
+    assert torch.allclose(got[mask], ref[mask], atol=1e-6, rtol=0), float((got[mask] - ref[mask]).abs().max())
+    assert bool((got[~mask] == 0).all())
