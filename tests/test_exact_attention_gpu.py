@@ -226,9 +226,12 @@ def test_deterministic_and_strictly_causal(cuda):
     assert not torch.equal(a1[:, :, 300:], a3[:, :, 300:])
 
 
-def test_full_benchmark_shape_every_head(cuda):
+@pytest.mark.parametrize("seed", [1234, 1235, 1236, 101234])
+def test_full_benchmark_shape_every_head(cuda, seed):
     """B=64, S=4096, H=16, D=64 causal (the attention-core workload), every
-    one of the 1024 (b, h) heads and every element checked.
+    one of the 1024 (b, h) heads and every element checked, on the harness's
+    accuracy seeds 1234+i and its timing seed 101234 (src/benchmark.py:80,
+    :185-192, :379).
 
     ``out`` starts as NaN, so a query tile the XCD-aware tile order never
     issues (or a row it never writes) fails the finiteness half of the rule.
@@ -239,7 +242,7 @@ def test_full_benchmark_shape_every_head(cuda):
     from techjam_amd.kernels import scaled_dot_product_attention
 
     b, s, h, d = 64, 4096, 16, 64
-    g = torch.Generator(device=cuda).manual_seed(101234)
+    g = torch.Generator(device=cuda).manual_seed(seed)
     q, k, v = (torch.randn(b, s, h, d, generator=g, device=cuda).transpose(1, 2) for _ in range(3))
     out = torch.full((b, s, h, d), float("nan"), device=cuda).transpose(1, 2)
     scaled_dot_product_attention(q, k, v, is_causal=True, out=out)
@@ -259,7 +262,7 @@ def test_full_benchmark_shape_every_head(cuda):
             del ref, err, ok
     finally:
         torch.set_float32_matmul_precision(prev)
-    print(f"attention core, all 1024 heads: failed={failed} max_abs={max_abs:.3e}")
+    print(f"attention core, seed {seed}, all 1024 heads: failed={failed} max_abs={max_abs:.3e}")
     assert failed == 0 and max_abs <= 4e-3
 
 

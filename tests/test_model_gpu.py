@@ -85,8 +85,9 @@ def test_config_1_one_layer_encoder(cuda):
 
 
 def test_config_2_packed_qkv_four_layers(cuda):
+    """The harness's five accuracy trials (seeds 1234+i, src/benchmark.py:80, :185-192)."""
     cfg = OracleConfig(8, 1024, 512, 8, 2048, 4, True)
-    _check(cfg, (1234, 1235), 0.5, cuda)
+    _check(cfg, range(1234, 1239), 0.5, cuda)
 
 
 @pytest.mark.parametrize("case_id", list(range(1, 14)))
@@ -117,12 +118,13 @@ def test_config_1_with_fp16_gemm_operands(cuda):
 
 def test_config_2_with_fp16_gemm_operands(cuda):
     cfg = OracleConfig(8, 1024, 512, 8, 2048, 4, True)
-    _check(cfg, (1234, 1235), 0.5, cuda, gemm_operands="fp16")
+    _check(cfg, range(1234, 1239), 0.5, cuda, gemm_operands="fp16")
 
 
 def test_config_4_with_fp16_gemm_operands(cuda):
     cfg = OracleConfig(2, 8192, 1024, 16, 4096, 4, True)
-    _check(cfg, (1234,), 0.5, cuda, oracle_on_gpu=True, oracle_cls=LinearMemoryReference, gemm_operands="fp16")
+    _check(cfg, range(1234, 1239), 0.5, cuda, oracle_on_gpu=True, oracle_cls=LinearMemoryReference,
+           gemm_operands="fp16")
 
 
 def test_fp16_gemm_operands_refuse_the_unfused_path(cuda):
@@ -147,8 +149,9 @@ def test_non_causal_right_padded_model(cuda):
 
 
 def test_config_4_long_sequence_on_the_linear_memory_oracle(cuda):
+    """The harness's five accuracy trials (seeds 1234+i)."""
     cfg = OracleConfig(2, 8192, 1024, 16, 4096, 4, True)
-    _check(cfg, (1234,), 0.5, cuda, oracle_on_gpu=True, oracle_cls=LinearMemoryReference)
+    _check(cfg, range(1234, 1239), 0.5, cuda, oracle_on_gpu=True, oracle_cls=LinearMemoryReference)
 
 
 @pytest.mark.parametrize("causal", [True, False])

@@ -238,13 +238,15 @@ def test_guarded_route_against_exact_attention(cuda):
 
 
 @pytest.mark.slow
-def test_extreme_length_workload_against_linear_memory_oracle(cuda):
-    """B=4, S=65536, H=16, D=64, fp32 io: zero failing elements, peak HBM < 8 GiB."""
+@pytest.mark.parametrize("seed", range(1234, 1239))
+def test_extreme_length_workload_against_linear_memory_oracle(cuda, seed):
+    """B=4, S=65536, H=16, D=64, fp32 io: zero failing elements, peak HBM < 8 GiB,
+    on the harness's five accuracy seeds (1234+i; the seed drives the q/k/v draw)."""
     from techjam_amd.implementations.poly_attention import guarded_attention
 
     b, s, h, d = 4, 65536, 16, 64
     torch.cuda.empty_cache()
-    g = torch.Generator(device=cuda).manual_seed(1234)
+    g = torch.Generator(device=cuda).manual_seed(seed)
     q = torch.randn(b, s, h, d, generator=g, device=cuda) * 0.5
     k = torch.randn(b, s, h, d, generator=g, device=cuda) * 0.5
     v = torch.randn(b, s, h, d, generator=g, device=cuda)
@@ -267,7 +269,7 @@ def test_extreme_length_workload_against_linear_memory_oracle(cuda):
         failed += nb
         mx = max(mx, m)
         del ref
-    print(f"extreme length: peak={peak / 2**30:.2f} GiB max_abs={mx:.3e} failed={failed}")
+    print(f"extreme length, seed {seed}: peak={peak / 2**30:.2f} GiB max_abs={mx:.3e} failed={failed}")
     assert failed == 0
 
 
