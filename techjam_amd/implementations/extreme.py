@@ -28,7 +28,7 @@ import torch.nn.functional as F
 from ..kernels.attention import scaled_dot_product_attention
 from ..model import fp16_weight
 from .poly_attention import guarded_attention
-from .poly_guard import poly_is_safe
+from .poly_guard import SIGMA_CEILING, poly_is_safe
 from .sdpa import StridedSDPASelfAttention
 
 CASE_6_CONFIG = (10000, 128, 128, 4, 128, True, 4)
@@ -145,10 +145,13 @@ class PolyOrExactSelfAttention(ExactOnlySelfAttention):
     def __init__(self, d_model: int, num_heads: int) -> None:
         super().__init__(d_model, num_heads)
         self.poly_enabled = POLY_ATTENTION_ENABLED
+        # The model-level ceiling: this module's output feeds the residual
+        # stream, and the reference calibrates the guard on the model's output.
+        self.sigma_ceiling = SIGMA_CEILING
         self.last_guard = None
 
     def route_name(self, sigma: Optional[float]) -> str:
-        return "poly" if self.poly_enabled and poly_is_safe(sigma) else "exact"
+        return "poly" if self.poly_enabled and poly_is_safe(sigma) and sigma <= self.sigma_ceiling else "exact"
 
     def context(self, x, valid_token_mask=None, causal=False, valid_len=None):
         self._check(x, valid_token_mask)
@@ -156,5 +159,6 @@ class PolyOrExactSelfAttention(ExactOnlySelfAttention):
             raise ValueError("the polynomial route is causal attention")
         b, s, _ = x.shape
         q, k, v = self.qkv(x)
-        ctx, self.last_guard = guarded_attention(q, k, v, self.scale, enabled=self.poly_enabled)
+        ctx, self.last_guard = guarded_attention(q, k, v, self.scale, enabled=self.poly_enabled,
+                                                 ceiling=self.sigma_ceiling)
         return ctx.transpose(1, 2).reshape(b, s, self.d_model)

@@ -21,7 +21,7 @@ import torch
 
 from ..kernels.attention import empty_like_heads, scaled_dot_product_attention
 from ..kernels.poly import poly_rows
-from .poly_guard import SIGMA_CEILING, guard, hermite_coefficients
+from .poly_guard import ATTENTION_SIGMA_CEILING, guard, hermite_coefficients
 
 CHUNK = 512
 EXACT_PREFIX = 4096
@@ -65,12 +65,16 @@ def guarded_attention(
     scale: float,
     *,
     enabled: bool = True,
-    ceiling: float = SIGMA_CEILING,
+    ceiling: float = ATTENTION_SIGMA_CEILING,
     out: Optional[torch.Tensor] = None,
 ):
     """Per-head guarded causal attention; returns ``(out, guard_result)``.
 
-    With ``enabled=False`` every head takes the exact kernel (the guard still
+    A head takes the polynomial route when its sampled score sigma is in
+    ``(0, ceiling]``. The default keeps the attention output itself within
+    the OR rule (``ATTENTION_SIGMA_CEILING``); the dispatcher's model module
+    passes the reference's model-level ``SIGMA_CEILING``. With
+    ``enabled=False`` every head takes the exact kernel (the guard still
     runs, to select split scores for wide-range heads).
     """
     g = guard(q, k, scale, ceiling=ceiling, exact_prefix=_prefix(q.shape[2]))

@@ -13,9 +13,23 @@ measurement runs in the HIP guard kernel, per ``(b, h)`` and on the device:
   Python float, one synchronisation), derived exactly from the per-head
   moments.
 
-``SIGMA_CEILING`` is the reference's calibrated 0.40: below the largest clean
-pass (0.4188) of its N=8192 sweep and above the benchmark's operating point
-(0.334).
+Two ceilings, for the two things a caller can require to stay within the
+benchmark's OR rule (|d| <= 2e-3 or 2 %):
+
+* ``SIGMA_CEILING`` = 0.40, the reference's calibration, for the model's
+  output (``src/implementations/poly_guard.py:22-65``: q/k projection weights
+  scaled in both models, the case-14 model's output against the dense
+  oracle). Re-measured with this build's kernels the same way: zero failing
+  elements through a per-head sigma of 0.489 at N = 8192 and 16384, first
+  failures at 0.52 -- 0.40 keeps its margin. The dispatcher's model route
+  uses it.
+* ``ATTENTION_SIGMA_CEILING`` = 0.29, for the attention output itself (every
+  head's output against exact fp32 attention, v ~ N(0, 1)), the default of
+  ``guarded_attention``. Largest clean pass 0.30 at N = 8192 .. 131072;
+  0.334 fails at N = 16384 (3 of 16.8 M elements) and 0.36 at 8192 -- and the
+  reference's scan restated in fp32 fails on the same elements, so that
+  boundary is the degree-2 fit's, not the kernel's. Attention feeding a
+  residual stream (the case above) tolerates more.
 """
 
 from __future__ import annotations
@@ -28,6 +42,7 @@ import torch
 from ..kernels.attention import GuardResult, score_guard
 
 SIGMA_CEILING = 0.40
+ATTENTION_SIGMA_CEILING = 0.29
 
 
 def guard(q: torch.Tensor, k: torch.Tensor, scale: float, *, samples: int = 512, seed: int = 0,
