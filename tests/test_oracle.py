@@ -288,7 +288,8 @@ def test_dense_model_padding_matches_torch_encoder_on_valid_rows():
     x = torch.randn(3, 40, 64, dtype=torch.float64).masked_fill(~mask[..., None], 0)
     causal = torch.nn.Transformer.generate_square_subsequent_mask(40, dtype=torch.float64)
     with torch.no_grad():
-        ref = enc(x, mask=causal, src_key_padding_mask=~mask, is_causal=True)
+        pad = torch.zeros(3, 40, dtype=torch.float64).masked_fill(~mask, float("-inf"))  # same type as `causal`
+        ref = enc(x, mask=causal, src_key_padding_mask=pad, is_causal=True)
         got = model(x, mask)
     assert torch.allclose(got[mask], ref[mask], atol=1e-6, rtol=0), float((got[mask] - ref[mask]).abs().max())
     assert bool((got[~mask] == 0).all())
