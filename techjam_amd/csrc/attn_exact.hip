@@ -257,6 +257,11 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
   int wave_last_key = a.causal ? min(qw0 + WROWS - 1, kv_end - 1) : kv_end - 1;
   if (qw0 >= L || qw0 >= row_cap) wave_last_key = -1;
 
+  // The first key tile's loads go out before q's, so the two latencies overlap.
+  KVStage<T, HD, BNT / 16> stage;
+  stage.init(a, b, h, tid);
+  if (n_kv > 0) stage.load(0, tid);
+
   // Q^T as the B operand: lane holds query qw0 + 32*qb + ln, dims 16*ks + 8*hl .. +7.
   half8_t qf[QB][TL::KS];
   half8_t qlo[QB][SPLIT ? TL::KS : 1];
@@ -320,12 +325,7 @@ __device__ __forceinline__ void attn_tile(const AttnArgs& a, SM& sm, int b, int 
       for (int r = 0; r < 16; ++r) oacc[qb][db][r] = 0.f;
   }
 
-  KVStage<T, HD, BNT / 16> stage;
-  stage.init(a, b, h, tid);
-  if (n_kv > 0) {
-    stage.load(0, tid);
-    stage.template store<SPLIT>(sm, 0, tid);
-  }
+  if (n_kv > 0) stage.template store<SPLIT>(sm, 0, tid);
   __syncthreads();
 
   for (int kt = 0; kt < n_kv; ++kt) {
@@ -529,6 +529,16 @@ __global__ __launch_bounds__(NT, (HD > 128 ? 1 : 2)) void attn_fwd_kernel(AttnAr
     if (j < nseq * a.n_mtiles) {
       bh = bh0 + j / a.n_mtiles;
       mrev = j % a.n_mtiles;
+      // An XCD hands consecutive workgroups to its four shader engines in
+      // turn and waits for the engine whose turn it is, so each engine must
+      // see the same work: heaviest-first in snake rounds of four (ranks
+      // 0 1 2 3, 7 6 5 4, 8 9 10 11, ...) gives engine i ranks i, 7-i, 8+i,
+      // 15-i, ..., equal sums, where plain heaviest-first gave the first
+      // engine the heaviest tile of every round.
+      if ((a.n_mtiles & 3) == 0) {
+        const int i = j & 3;
+        mrev = (mrev & ~3) + (((j >> 2) & 1) ? 3 - i : i);
+      }
     } else {
       const int r = j - nseq * a.n_mtiles;
       const int per_group = a.group * a.n_mtiles;
