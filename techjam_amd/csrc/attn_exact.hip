@@ -34,7 +34,10 @@
 //     Launches with row limits, whose work sits on a few (b, h), and launches
 //     with fewer than eight (b, h) spread every (b, h) over all XCDs.
 //     The (b, h) ranges are taken in sample-fastest order, so each XCD holds
-//     an even mix of the samples' valid lengths.
+//     an even mix of the samples' valid lengths. Both walks deal their
+//     heaviest-first lists in snake rounds of four, so that the XCD's four
+//     shader engines, which take consecutive workgroups in turn, see equal
+//     work.
 //   * Heads flagged in qk_split compute QK^T from a two-term fp16 expansion of
 //     q and k (x = hi + lo, both fp16) with three MFMAs -- hi.hi + hi.lo +
 //     lo.hi -- which restores fp32-level score accuracy where the score range
@@ -544,7 +547,14 @@ __global__ __launch_bounds__(NT, (HD > 128 ? 1 : 2)) void attn_fwd_kernel(AttnAr
       const int per_group = a.group * a.n_mtiles;
       const int g0 = nseq + r / per_group * a.group;
       if (g0 >= nb) return;
-      const int rr = r % per_group;
+      // Position rr of the group's heaviest-first list (rank rr / gs of
+      // (b, h) rr % gs), dealt in the same snake rounds: with two (b, h) per
+      // group, plain order gave two engines the heavier rank of every pair.
+      int rr = r % per_group;
+      if ((a.n_mtiles & 3) == 0) {
+        const int i = rr & 3;
+        rr = (rr & ~3) + (((rr >> 2) & 1) ? 3 - i : i);
+      }
       const int gs = min(a.group, nb - g0);
       mrev = rr / gs;
       if (mrev >= a.n_mtiles) return;
