@@ -266,6 +266,53 @@ def test_full_benchmark_shape_every_head(cuda, seed):
     assert failed == 0 and max_abs <= 4e-3
 
 
+# One shape per branch of the kernel's tile order (B, H, S, valid lengths):
+# query tiles per (b, h) = S / 256 when B*H*S/256 >= 1024, else S / 128; a
+# group holds max(1, 64 / tiles) (b, h); an XCD owns B*H/8 of them, walks all
+# but the last group one (b, h) at a time when it owns more than two groups,
+# and deals each list in snake rounds of four when the tile count allows.
+_ORDER_CASES = {
+    "per-head-snake-then-group-of-4": (5, 16, 4096, None),   # 16 tiles, 10 (b, h) per XCD
+    "groups-of-2": (2, 16, 8192, None),                       # 32 tiles, 4 (b, h) per XCD
+    "groups-of-2-ragged": (2, 16, 8192, [8192, 5000]),
+    "groups-of-1": (1, 16, 16384, None),                      # 64 tiles, 2 (b, h) per XCD
+    "full-and-partial-group": (3, 8, 4096, None),             # 128-row tiles: 32, 3 (b, h) per XCD
+    "tile-count-not-multiple-of-4": (4, 8, 2900, None),       # 128-row tiles: 23
+}
+
+
+@pytest.mark.parametrize("name", list(_ORDER_CASES))
+def test_every_tile_order_issues_every_query_tile(cuda, name):
+    """``out`` starts as NaN: a query tile that a branch of the XCD /
+    shader-engine tile order skipped or issued twice with another's rows
+    would leave NaN or wrong rows. Every element against the blockwise
+    oracle (fp32 on the GPU, matmul precision "highest")."""
+    from techjam_amd.kernels import scaled_dot_product_attention
+
+    b, h, s, lengths = _ORDER_CASES[name]
+    d = 64
+    g = torch.Generator(device=cuda).manual_seed(4242)
+    q, k, v = (torch.randn(b, s, h, d, generator=g, device=cuda).transpose(1, 2) for _ in range(3))
+    vl = None if lengths is None else torch.tensor(lengths, dtype=torch.int32, device=cuda)
+    out = torch.full((b, s, h, d), float("nan"), device=cuda).transpose(1, 2)
+    scaled_dot_product_attention(q, k, v, is_causal=True, valid_len=vl, out=out)
+    torch.cuda.synchronize()
+    prev = torch.get_float32_matmul_precision()
+    torch.set_float32_matmul_precision("highest")
+    try:
+        ref = blockwise_attention(q, k, v, d ** -0.5, True, valid_len=vl, block_q=1024, block_k=1024)
+    finally:
+        torch.set_float32_matmul_precision(prev)
+    err = (out - ref).abs()
+    ok = torch.isfinite(out) & ((err <= ATOL) | (err <= RTOL * ref.abs()))
+    bad = int((~ok).sum())
+    print(f"{name}: B={b} H={h} S={s}: failed={bad} max_abs={float(torch.nan_to_num(err, nan=float('inf')).max()):.3e}")
+    assert bad == 0
+    if lengths is not None:
+        for bi, n in enumerate(lengths):
+            assert torch.count_nonzero(out[bi, :, n:]).item() == 0
+
+
 def _sweep_cases(n, seed):
     """Seeded random configurations: shape, head dim, causality, dtype,
     layout ([B, S, H, D] storage viewed as [B, H, S, D], or contiguous), valid
