@@ -45,8 +45,13 @@ FLAGS = [
 
 # Per-file additions. The exact-attention kernel never needs IEEE NaN
 # semantics in its row maxima (scores are finite or -inf), and without them
-# fmaxf chains compile to v_max3 with no canonicalising moves.
-FILE_FLAGS = {"attn_exact.hip": ["-fno-honor-nans"]}
+# fmaxf chains compile to v_max3 with no canonicalising moves. Its split-score
+# instance with two query blocks per wave is scheduled by LLVM's max-ILP
+# strategy (faster for it; the default scheduler is faster for the others).
+FILE_FLAGS = {
+    "attn_exact.hip": ["-fno-honor-nans"],
+    "attn_exact_split.hip": ["-fno-honor-nans", "-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+}
 
 
 def sources():
