@@ -524,12 +524,28 @@ __global__ __launch_bounds__(NT, (HD > 128 ? 1 : 2)) void attn_fwd_kernel(AttnAr
   if (a.balanced) {
     // Row limits concentrate the work on a few (b, h) (e.g. the exact
     // fallback heads of the guarded polynomial route). Query tiles are then
-    // issued heaviest first across all (b, h), with the (b, h) index rotated
-    // per query tile so that consecutive ids -- which the hardware deals out
-    // round-robin over the XCDs -- spread each (b, h) over every XCD.
+    // issued heaviest first across all (b, h): slot s of rank mrev is id s
+    // + mrev * bhn, on XCD s % 8 and, within the XCD, shader engine
+    // (mrev * bhn / 8 + s / 8) % 4. With bhn a multiple of 8, (b, h) = 8 g + c
+    // takes the slot whose group s / 8 is g + mrev and whose XCD is c + the
+    // base-8 digit sum of g + mrev / 4: four consecutive ranks of one (b, h)
+    // share an XCD (and its L2 copy of that head's K/V), every (b, h) moves
+    // on to the next XCD after them, (b, h) whose indices differ in any
+    // base-8 digit above the lowest (heads 0, 16, 32, 48 ...) sit on
+    // different XCDs, and the shader engine turns with the rank. Either
+    // way a rank's slots are a permutation of the (b, h).
     const int bhn = a.B * a.H;
     const int mrev = id / bhn;
-    bh = (id % bhn + mrev) % bhn;
+    const int s = id % bhn;
+    if ((bhn & 7) == 0) {
+      const int ng = bhn >> 3;
+      const int g = ((s >> 3) - mrev % ng + ng) % ng;
+      int digits = 0;
+      for (int t = g; t > 0; t >>= 3) digits += t;
+      bh = 8 * g + ((s - mrev / 4 - digits) & 7);
+    } else {
+      bh = (s + mrev) % bhn;
+    }
     mt = a.n_mtiles - 1 - mrev;
   } else {
     // XCD x owns (b, h) bh0 .. bh0 + nb - 1 (range sizes differ by at most
