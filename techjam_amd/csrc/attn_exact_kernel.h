@@ -530,10 +530,11 @@ __global__ __launch_bounds__(NT, (HD > 128 ? 1 : 2)) void attn_fwd_kernel(AttnAr
     // takes the slot whose group s / 8 is g + mrev and whose XCD is c + the
     // base-8 digit sum of g + mrev / 4: four consecutive ranks of one (b, h)
     // share an XCD (and its L2 copy of that head's K/V), every (b, h) moves
-    // on to the next XCD after them, (b, h) whose indices differ in any
-    // base-8 digit above the lowest (heads 0, 16, 32, 48 ...) sit on
-    // different XCDs, and the shader engine turns with the rank. Either
-    // way a rank's slots are a permutation of the (b, h).
+    // on to the next XCD after them, (b, h) with the same c whose g differ
+    // in digit sum mod 8 (heads 0, 16, 32, 48, ...: every B-th of a
+    // multiple-of-8 H) sit on different XCDs, and the shader engine turns
+    // with the rank. Either way a rank's slots are a permutation of the
+    // (b, h).
     const int bhn = a.B * a.H;
     const int mrev = id / bhn;
     const int s = id % bhn;
