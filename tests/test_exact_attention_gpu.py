@@ -131,6 +131,45 @@ def test_row_limit_leaves_other_rows_untouched(cuda):
         assert bool((got[bi, hi, n:] == 12345.0).all()), f"head {bh} rows >= {n} were written"
 
 
+# Launches with row limits take the balanced tile order: (b, h) spread over
+# the XCDs by their index digits, four ranks of a (b, h) per XCD, when B*H is
+# a multiple of 8, and a plain rotation otherwise. (B, H, S): 128-row tiles
+# below 1024 wide tiles, 256-row tiles at B=4 H=16 S=4096.
+_ROW_LIMIT_ORDER_CASES = [(1, 8, 4096), (3, 8, 2048), (4, 16, 4096), (3, 4, 1500)]
+
+
+@pytest.mark.parametrize("b,h,s", _ROW_LIMIT_ORDER_CASES, ids=lambda x: str(x))
+def test_row_limited_tile_order_issues_every_query_tile(cuda, b, h, s):
+    """NaN-prefilled output, a mix of per-head row limits (0, a 4096-row
+    prefix, S, and odd values): every row below its head's limit against the
+    blockwise oracle, every row at or past it still NaN."""
+    from techjam_amd.kernels import scaled_dot_product_attention
+
+    d = 64
+    g = torch.Generator(device=cuda).manual_seed(5150)
+    q, k, v = (torch.randn(b, s, h, d, generator=g, device=cuda).transpose(1, 2) for _ in range(3))
+    choices = [s, min(s, 4096), 0, s - 1, (s // 3) | 1, 257]
+    limits = torch.tensor([choices[i % len(choices)] for i in range(b * h)], dtype=torch.int32, device=cuda)
+    out = torch.full((b, s, h, d), float("nan"), device=cuda).transpose(1, 2)
+    scaled_dot_product_attention(q, k, v, is_causal=True, row_limit=limits, out=out)
+    torch.cuda.synchronize()
+    prev = torch.get_float32_matmul_precision()
+    torch.set_float32_matmul_precision("highest")
+    try:
+        ref = blockwise_attention(q, k, v, d ** -0.5, True, block_q=1024, block_k=1024)
+    finally:
+        torch.set_float32_matmul_precision(prev)
+    bad = 0
+    for bh, n in enumerate(limits.tolist()):
+        bi, hi = divmod(bh, h)
+        got, want = out[bi, hi, :n], ref[bi, hi, :n]
+        err = (got - want).abs()
+        ok = torch.isfinite(got) & ((err <= ATOL) | (err <= RTOL * want.abs()))
+        bad += int((~ok).sum())
+        assert bool(torch.isnan(out[bi, hi, n:]).all()), f"head {bh}: rows >= {n} were written"
+    assert bad == 0, f"{bad} failing elements"
+
+
 def test_packed_qkv_strided_views(cuda):
     """q, k, v as views of one [B, S, 3, H, D] projection; output into [B, S, H, D]."""
     b, s, h, d = 2, 333, 4, 64
